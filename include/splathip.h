@@ -1,0 +1,152 @@
+/* splathip: MI355X-native (gfx950) feed-forward reconstruction network path of
+ * antoineMoPa/splatting-rs (Depth Anything 3 and MapAnything forward), as a C ABI.
+ *
+ * Each entry point below replaces a reference Rust entry point, named in its comment
+ * (file:line under the reference tree). Nothing panics or unwinds across this ABI: every
+ * function returns a splat_status and leaves a message for splat_last_error().
+ *
+ * Threading: a context is not thread-safe; the caller serialises calls on it (the reference's
+ * model is used from one thread, depthanything3-rs/src/pipeline.rs:58-73). Contexts are
+ * independent; each owns one HIP stream on its device, the loaded weights and an
+ * activation arena that grows to the largest input seen.
+ *
+ * Tensors: images are [V, 3, H, W] float32, ImageNet-normalised, H and W multiples of 14.
+ * Host-pointer entry points copy inputs in and outputs out and synchronise before
+ * returning. *_device entry points take device pointers (HIP memory on the context's
+ * device) and only enqueue on the context's stream (splat_stream); call
+ * splat_synchronize or synchronise the stream before reading the outputs.
+ */
+#ifndef SPLATHIP_H
+#define SPLATHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct splat_ctx splat_ctx;
+
+typedef enum splat_status {
+  SPLAT_OK = 0,
+  SPLAT_BAD_ARGUMENT = 1,
+  SPLAT_BAD_SHAPE = 2,      /* H or W not a multiple of 14, views of unequal size, ... */
+  SPLAT_MISSING_KEY = 3,    /* a checkpoint tensor is absent */
+  SPLAT_SHAPE_MISMATCH = 4, /* a checkpoint tensor has the wrong shape */
+  SPLAT_HIP_ERROR = 5,
+  SPLAT_NONFINITE = 6,      /* output not finite / depth not positive (outputs still written) */
+  SPLAT_IO_ERROR = 7,
+  SPLAT_NOT_LOADED = 8
+} splat_status;
+
+typedef enum splat_dtype { SPLAT_F32 = 0, SPLAT_BF16 = 1, SPLAT_F16 = 2 /* computed as bf16 */ } splat_dtype;
+
+/* depthanything3-rs/src/variant.rs:17-23 */
+typedef enum splat_da3_variant { SPLAT_DA3_SMALL = 0, SPLAT_DA3_BASE = 1, SPLAT_DA3_LARGE = 2, SPLAT_DA3_GIANT = 3 } splat_da3_variant;
+
+/* depthanything3-rs/src/reference_view.rs:14-22 */
+typedef enum splat_ref_strategy { SPLAT_REF_FIRST = 0, SPLAT_REF_MIDDLE = 1, SPLAT_REF_SADDLE_BALANCED = 2 } splat_ref_strategy;
+
+/* depthanything3-rs/src/model.rs:26-34 (Stage::{Block(i), DenseHead, CameraHead}) */
+typedef enum splat_stage { SPLAT_STAGE_BLOCK = 0, SPLAT_STAGE_DENSE_HEAD = 1, SPLAT_STAGE_CAMERA_HEAD = 2 } splat_stage;
+
+/* Progress = &mut dyn FnMut(Stage), depthanything3-rs/src/model.rs:34. Called on the calling
+ * thread as each stage is enqueued. */
+typedef void (*splat_progress_fn)(int stage, int block, void* user);
+
+/* Debug tap: the residual stream [rows, dim] (float32, host memory valid during the call)
+ * after backbone / encoder / info-sharing block `block` (blocks numbered across stages).
+ * Forces a synchronisation per block. */
+typedef void (*splat_tap_fn)(int block, const float* hidden, int rows, int dim, void* user);
+
+/* MapAnything widths. The reference hard-codes them (mapanything-rs/src/dinov2.rs:8-17,
+ * info_sharing.rs:12-14, dpt.rs:10-14, heads.rs:9-15); ffn: 0 = GELU MLP, 1 = SwiGLU. */
+typedef struct splat_ma_spec {
+  int enc_dim, enc_heads, enc_depth, enc_ffn, enc_hidden;
+  int info_dim, info_heads, info_depth, info_ffn, info_hidden;
+  int hooks[3];           /* info blocks whose normed output feeds the dense head; last = depth-1 */
+  int dpt_dims[4];        /* 1x1 projection widths per hook */
+  int dpt_features;       /* fusion width */
+  int pose_dim;           /* pose head width */
+  int scale_dim;          /* scale head width */
+} splat_ma_spec;
+
+/* Outputs of splat_da3_forward_raw: RawPrediction, depthanything3-rs/src/model.rs:37-49.
+ * Caller-owned buffers; NULL skips an optional output. R = H/14, C = W/14. */
+typedef struct splat_da3_out {
+  float* depth;          /* [V, H, W]  exp(logit)                                         */
+  float* depth_conf;     /* [V, H, W]  1 + exp(logit)                                     */
+  float* ray_logits;     /* [V, 7, 8R, 8C] (optional)                                     */
+  float* pose_encoding;  /* [V, 9] t(3), quaternion xyzw (4), fov (2)                      */
+  float* camera_tokens;  /* [V, 2*dim] (optional)                                         */
+  int32_t reference_view;/* written by the call                                           */
+} splat_da3_out;
+
+/* Outputs of splat_ma_forward: MapAnything::forward's ViewOutput list
+ * (mapanything-rs/src/model.rs:21-34, 86-144) plus the raw dense head output. */
+typedef struct splat_ma_out {
+  float* raw;            /* [V, 6, H, W] dense head output before activation (optional)   */
+  float* quaternion;     /* [V, 4] unit (x, y, z, w), camera to world                      */
+  float* translation;    /* [V, 3] metric (times the scale)                                */
+  float* scale;          /* [1] metric scale                                               */
+  float* points;         /* [V, H, W, 3] camera-frame points (optional)                    */
+  float* conf;           /* [V, H, W] 1 + exp(raw conf) (optional)                         */
+  uint8_t* mask;         /* [V, H, W] unambiguous (raw mask logit > 0) (optional)          */
+} splat_ma_out;
+
+/* --- context ------------------------------------------------------------------------------ */
+
+/* Replaces candle's `Device::new_metal(0)` / `Device::Cpu` choice (depthanything3-rs/src/main.rs:136). */
+int splat_create(int hip_device, splat_ctx** out);
+void splat_destroy(splat_ctx* ctx);
+/* Last error message of the context ("" when none). With ctx == NULL: of the last failed splat_create. */
+const char* splat_last_error(const splat_ctx* ctx);
+/* The context's hipStream_t, for event timing and device-pointer entry points. */
+void* splat_stream(splat_ctx* ctx);
+int splat_synchronize(splat_ctx* ctx);
+/* 1 = capture each forward shape into a HIP graph on first use and replay it (default 0).
+ * Ignored while progress callbacks or debug taps are set. */
+int splat_set_graphs(splat_ctx* ctx, int enable);
+/* Per-block residual taps (NULL to disable); replaces nothing in the reference: a test hook. */
+int splat_set_debug_taps(splat_ctx* ctx, splat_tap_fn fn, void* user);
+
+/* --- Depth Anything 3 ------------------------------------------------------------------------ */
+
+/* weights::load_model(variant, strategy, Some(path), dtype, device), depthanything3-rs/src/weights.rs:26-48
+ * (tensors under the `model.` prefix, every shape checked as DepthAnything3::new does,
+ * depthanything3-rs/src/model.rs:85-94). */
+int splat_load_da3(splat_ctx* ctx, const char* safetensors_path, int variant, int dtype, int ref_strategy);
+/* weights::model_from_safetensors_bytes, depthanything3-rs/src/weights.rs:51-60 (bytes are copied). */
+int splat_load_da3_bytes(splat_ctx* ctx, const uint8_t* bytes, size_t len, int variant, int dtype, int ref_strategy);
+/* DepthAnything3::forward_raw_with_progress, depthanything3-rs/src/model.rs:101-123 (progress may be NULL). */
+int splat_da3_forward_raw(splat_ctx* ctx, const float* images, int V, int H, int W, splat_progress_fn progress,
+                          void* user, splat_da3_out* out);
+/* Same with device pointers in `images` and in every non-NULL field of `out` except
+ * reference_view, which is written to *ref_view_device (int32 device memory) when not NULL. */
+int splat_da3_forward_raw_device(splat_ctx* ctx, const float* images, int V, int H, int W, splat_da3_out* out,
+                                 int32_t* ref_view_device);
+
+/* --- MapAnything ----------------------------------------------------------------------------- */
+
+/* MapAnything::new(VarBuilder over the checkpoint), mapanything-rs/src/model.rs:69-81;
+ * spec NULL = the reference's constants. */
+int splat_load_mapanything(splat_ctx* ctx, const char* safetensors_path, const splat_ma_spec* spec, int dtype);
+int splat_load_mapanything_bytes(splat_ctx* ctx, const uint8_t* bytes, size_t len, const splat_ma_spec* spec, int dtype);
+/* The reference's constants (spec NULL above). */
+void splat_ma_reference_spec(splat_ma_spec* out);
+/* MapAnything::forward(images, intrinsics), mapanything-rs/src/model.rs:86-144, for views of
+ * one size. intrinsics must be NULL (the known-intrinsics ray encoder is not implemented:
+ * SPLAT_BAD_ARGUMENT otherwise). */
+int splat_ma_forward(splat_ctx* ctx, const float* images, int V, int H, int W, const double* intrinsics,
+                     splat_ma_out* out);
+int splat_ma_forward_device(splat_ctx* ctx, const float* images, int V, int H, int W, splat_ma_out* out);
+/* Dinov2::forward for every view (mapanything-rs/src/dinov2.rs:129-145): tokens [V, 1+R*C, enc_dim]. */
+int splat_ma_encode(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens);
+int splat_ma_encode_device(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPLATHIP_H */

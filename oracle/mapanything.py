@@ -1,0 +1,174 @@
+"""CPU oracle for MapAnything — TEST INFRASTRUCTURE ONLY (see oracle/common.py).
+
+Restates mapanything-rs/src/{model,dinov2,vit_block,info_sharing,dpt,heads}.rs in torch-CPU
+float32, parameterised by a spec (splathip.specs.MaSpec) so that the reference's constants
+and the benchmark's ViT-L / 768 widths both run. With enc_dim != info_dim the assumed
+`info_sharing.proj_embed` Linear maps the fused patches and raw class token to info_dim.
+"""
+from __future__ import annotations
+
+from typing import Dict
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import common as C
+
+LN_EPS = 1e-6           # mapanything-rs/src/vit_block.rs:8
+RAY_MIN_NORM = 1e-8     # mapanything-rs/src/model.rs:17
+CONF_MIN = 1.0          # mapanything-rs/src/model.rs:19
+QUAT_MIN_NORM = 1e-8    # mapanything-rs/src/heads.rs:16
+MIN_SCALE = 1e-8        # mapanything-rs/src/heads.rs:17
+
+
+def encoder_forward(p, spec, images, taps=None):
+    """mapanything-rs/src/dinov2.rs:129-145, all views batched (each view is independent)."""
+    V, _, H, W = images.shape
+    R, Cc = H // C.PATCH, W // C.PATCH
+    e = "encoder.model"
+    patches = C.conv(images, p, e + ".patch_embed.proj", stride=C.PATCH).flatten(2).transpose(1, 2)
+    pos = C.positional_embedding(p[e + ".pos_embed"], R, Cc).to(images.dtype)
+    xs = torch.cat([p[e + ".cls_token"].expand(V, 1, spec.enc_dim), patches], 1) + pos
+    for i in range(spec.enc_depth):
+        xs = C.vit_block(xs, p, f"{e}.blocks.{i}", spec.enc_ffn == 1, LN_EPS)
+        if taps is not None:
+            taps.append(xs.clone())
+    return xs
+
+
+def info_sharing_forward(p, spec, patches, classes, taps=None):
+    """mapanything-rs/src/info_sharing.rs:50-102. patches [V, P, d], classes [V, 1, d]."""
+    V, P, d = patches.shape
+    n = P + 1
+    q = "info_sharing"
+    seq = torch.cat([patches, classes], 1)                       # per view [patches, class]
+    seq = torch.cat([seq[:1] + p[q + ".view_pos_table"][0], seq[1:]], 0)
+    xs = torch.cat([seq.reshape(1, V * n, d), p["scale_token"].reshape(1, 1, d)], 1)
+    stored = []
+    for i in range(spec.info_depth):
+        name = f"{q}.self_attention_blocks.{i}"
+        if i % 2 == 0:
+            xs = C.vit_block(xs, p, name, spec.info_ffn == 1, LN_EPS)
+        else:
+            per_view = xs[:, :V * n].reshape(V, n, d)
+            att = C.vit_block(per_view, p, name, spec.info_ffn == 1, LN_EPS).reshape(1, V * n, d)
+            xs = torch.cat([att, xs[:, V * n:]], 1)
+        if taps is not None:
+            taps.append(xs.clone())
+        if i in spec.hooks:
+            stored.append(C.layer_norm(xs, p[q + ".norm.weight"], p[q + ".norm.bias"], LN_EPS))
+    per_view = [[s[0, v * n: v * n + P] for s in stored] for v in range(V)]
+    return per_view, stored[2][0, V * n]
+
+
+def _rcu(x, p, name):
+    """mapanything-rs/src/dpt.rs:94-113"""
+    out = C.conv(F.relu(x), p, name + ".conv1", padding=1)
+    out = C.conv(F.relu(out), p, name + ".conv2", padding=1)
+    return out + x
+
+
+def _fusion(x, skip, p, name):
+    """mapanything-rs/src/dpt.rs:116-140: out_conv(up2x(RCU2(x + RCU1(skip))))"""
+    if skip is not None:
+        x = x + _rcu(skip, p, name + ".resConfUnit1")
+    y = _rcu(x, p, name + ".resConfUnit2")
+    y = C.resize_bilinear(y, 2 * y.shape[2], 2 * y.shape[3])
+    return C.conv(y, p, name + ".out_conv")
+
+
+def dpt_forward(p, spec, hooks, R, Cc):
+    """mapanything-rs/src/dpt.rs:174-199, views batched. hooks: 4 tensors [V, P, dim]."""
+    pyr = []
+    for h, tok in enumerate(hooks):
+        V, P, D = tok.shape
+        x = tok.transpose(1, 2).reshape(V, D, R, Cc)
+        hp = f"dense_head.0.input_process.{h}"
+        x = C.conv(x, p, hp + ".0.0")
+        if h == 0:
+            x = C.conv_t(x, p, hp + ".0.1", 4)
+        elif h == 1:
+            x = C.conv_t(x, p, hp + ".0.1", 2)
+        elif h == 3:
+            x = C.conv(x, p, hp + ".0.1", padding=1, stride=2)
+        pyr.append(C.conv(x, p, hp + ".1", padding=1))
+    path = _fusion(pyr[3], None, p, "dense_head.0.scratch.refinenet4")
+    for level in (2, 1, 0):
+        h, w = pyr[level].shape[2], pyr[level].shape[3]
+        path = path[:, :, :h, :w]
+        path = _fusion(path, pyr[level], p, f"dense_head.0.scratch.refinenet{level + 1}")
+    out = C.conv(path, p, "dense_head.1.conv1", padding=1)
+    out = C.resize_bilinear(out, R * C.PATCH, Cc * C.PATCH)
+    return C.conv(F.relu(C.conv(out, p, "dense_head.1.conv2.0", padding=1)), p, "dense_head.1.conv2.2")
+
+
+def pose_head(p, spatial):
+    """mapanything-rs/src/heads.rs:80-99. spatial [V, d, h, w] -> (t [V,3], unit q [V,4])."""
+    x = C.conv(spatial, p, "pose_head.proj")
+    for blk in range(2):
+        r = x
+        for k in range(1, 4):
+            r = F.relu(C.conv(r, p, f"pose_head.res_conv.{blk}.res_conv{k}"))
+        x = x + r
+    pooled = x.flatten(2).mean(-1)
+    for name in ("more_mlps.0", "more_mlps.2"):
+        pooled = F.relu(C.linear(pooled, p, "pose_head." + name))
+    quat = C.linear(pooled, p, "pose_head.fc_rot")
+    norm = quat.pow(2).sum(-1, keepdim=True).sqrt().clamp(min=QUAT_MIN_NORM)
+    return C.linear(pooled, p, "pose_head.fc_t"), quat / norm
+
+
+def scale_head(p, token):
+    """mapanything-rs/src/heads.rs:122-129"""
+    x = C.linear(token, p, "scale_head.proj")
+    for layer in range(2):
+        x = F.relu(C.linear(x, p, f"scale_head.mlp.{layer}.0"))
+    return torch.exp(C.linear(x, p, "scale_head.output_proj")).clamp(min=MIN_SCALE).flatten()
+
+
+def dense_output(raw, scale):
+    """mapanything-rs/src/model.rs:148-172 for [V, 6, H, W] raw maps."""
+    rays = raw[:, 0:3]
+    norm = rays.pow(2).sum(1, keepdim=True).sqrt().clamp(min=RAY_MIN_NORM)
+    depth = torch.exp(raw[:, 3:4]) * scale
+    points = rays / norm * depth
+    return points, CONF_MIN + torch.exp(raw[:, 4]), raw[:, 5] > 0
+
+
+def forward(weights, spec, images, dtype=torch.float32, encoder_only=False, taps=None, info_taps=None) -> dict:
+    """mapanything-rs/src/model.rs:86-144 with no intrinsics (the `None` branch at :103)."""
+    p = C.to_torch(weights, dtype) if not isinstance(next(iter(weights.values())), torch.Tensor) else weights
+    x = torch.as_tensor(np.asarray(images)).to(dtype)
+    V, _, H, W = x.shape
+    R, Cc = H // C.PATCH, W // C.PATCH
+    P = R * Cc
+    with torch.no_grad():
+        tokens = encoder_forward(p, spec, x, taps)
+        if encoder_only:
+            return {"encoder_tokens": tokens.float()}
+        fused = C.layer_norm(tokens[:, 1:], p["fusion_norm_layer.weight"], p["fusion_norm_layer.bias"], LN_EPS)
+        classes = tokens[:, :1]
+        info_patches, info_classes = fused, classes
+        if spec.has_proj:
+            info_patches = C.linear(fused, p, "info_sharing.proj_embed")
+            info_classes = C.linear(classes, p, "info_sharing.proj_embed")
+        per_view, scale_tok = info_sharing_forward(p, spec, info_patches, info_classes, info_taps)
+        scale = scale_head(p, scale_tok[None])[0]
+        hooks = [fused] + [torch.stack([pv[k] for pv in per_view]) for k in range(3)]
+        raw = dpt_forward(p, spec, hooks, R, Cc).float()
+        last = hooks[3]
+        spatial = last.transpose(1, 2).reshape(V, spec.info_dim, R, Cc)
+        trans, quat = pose_head(p, spatial)
+        points, conf, mask = dense_output(raw, scale.float())
+    return {
+        "raw": raw,
+        "scale": float(scale),
+        "quaternion": quat.float(),
+        "translation": (trans.float() * scale.float()),
+        "translation_raw": trans.float(),
+        "points": points.float(),
+        "conf": conf.float(),
+        "mask": mask,
+        "encoder_tokens": tokens.float(),
+    }

@@ -1,0 +1,349 @@
+// The C ABI (include/splathip.h): argument checks, error mapping and host<->device staging
+// around the models. Nothing throws across this boundary.
+#include <cmath>
+#include <cstring>
+
+#include "runtime.h"
+#include "../../include/splathip_kernels.h"
+
+using namespace splat;
+
+namespace {
+
+thread_local std::string g_create_error;
+
+Context* C(splat_ctx* c) { return reinterpret_cast<Context*>(c); }
+
+template <typename F>
+int guard(Context* ctx, F&& fn) {
+  if (!ctx) return BAD_ARGUMENT;
+  try {
+    SPLAT_HIP(hipSetDevice(ctx->device));
+    fn();
+    ctx->last_error.clear();
+    return OK;
+  } catch (const Error& e) {
+    ctx->last_error = e.what();
+    return e.code;
+  } catch (const std::exception& e) {
+    ctx->last_error = e.what();
+    return HIP_ERROR;
+  } catch (...) {
+    ctx->last_error = "unknown error";
+    return HIP_ERROR;
+  }
+}
+
+int model_dtype(int dtype) {
+  SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16 || dtype == SPLAT_F16, BAD_ARGUMENT, "unknown dtype");
+  return dtype == SPLAT_F32 ? F32 : BF16;
+}
+
+void check_images(const float* images, int V, int H, int W) {
+  SPLAT_CHECK(images != nullptr, BAD_ARGUMENT, "images is NULL");
+  SPLAT_CHECK(V >= 1, BAD_SHAPE, "no views");
+  SPLAT_CHECK(H >= 14 && W >= 14 && H % 14 == 0 && W % 14 == 0, BAD_SHAPE,
+              "image " + std::to_string(W) + "x" + std::to_string(H) + " is not a multiple of the 14 px patch");
+}
+
+void* staging(Context* ctx, int slot, size_t bytes) { return ctx->staging_buffer(slot, bytes); }
+
+bool use_graphs(Context* ctx) { return ctx->graphs && !ctx->hooks.tap && !ctx->hooks.progress; }
+
+void da3_device(Context* ctx, const float* images, int V, int H, int W, const splat_da3_out& out, int32_t* ref) {
+  SPLAT_CHECK(ctx->da3 != nullptr, NOT_LOADED, "no Depth Anything 3 model loaded");
+  check_images(images, V, H, W);
+  SPLAT_CHECK(out.depth && out.depth_conf && out.pose_encoding, BAD_ARGUMENT, "depth, depth_conf and pose_encoding are required");
+  ctx->da3->prepare(V, H, W);
+  Context::GraphKey key{0, V, H, W, images, {out.depth, out.depth_conf, out.ray_logits, out.pose_encoding, out.camera_tokens, ref}};
+  ctx->run(key, use_graphs(ctx), [&] { ctx->da3->forward(images, V, H, W, out, ref, ctx->hooks); });
+}
+
+void ma_device(Context* ctx, const float* images, int V, int H, int W, const splat_ma_out& out, float* tokens,
+               bool encoder_only) {
+  SPLAT_CHECK(ctx->ma != nullptr, NOT_LOADED, "no MapAnything model loaded");
+  check_images(images, V, H, W);
+  ctx->ma->prepare(V, H, W);
+  Context::GraphKey key{encoder_only ? 2 : 1, V, H, W, images,
+                        {out.raw, out.quaternion, out.translation, out.scale, out.points, out.conf, out.mask, tokens}};
+  ctx->run(key, use_graphs(ctx), [&] { ctx->ma->forward(images, V, H, W, out, tokens, encoder_only, ctx->hooks); });
+}
+
+void load_ma(Context* ctx, SafeTensors& st, const splat_ma_spec* spec, int dtype) {
+  splat_ma_spec s;
+  if (spec) s = *spec;
+  else splat_ma_reference_spec(&s);
+  const int dt = model_dtype(dtype);
+  ctx->clear_graphs();
+  ctx->ma.reset();
+  ctx->ma = std::make_unique<MaModel>(*ctx, st, s, dt);
+}
+
+void load_da3(Context* ctx, SafeTensors& st, int variant, int dtype, int strategy) {
+  const int dt = model_dtype(dtype);
+  ctx->clear_graphs();
+  ctx->da3.reset();
+  ctx->da3 = std::make_unique<Da3Model>(*ctx, st, variant, dt, strategy);
+}
+
+template <typename T>
+void d2h(Context* ctx, T* host, const void* dev, size_t count) {
+  if (host) SPLAT_HIP(hipMemcpyAsync(host, dev, count * sizeof(T), hipMemcpyDeviceToHost, ctx->stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int splat_create(int hip_device, splat_ctx** out) {
+  if (!out) return BAD_ARGUMENT;
+  *out = nullptr;
+  try {
+    *out = reinterpret_cast<splat_ctx*>(new Context(hip_device));
+    return OK;
+  } catch (const Error& e) {
+    g_create_error = e.what();
+    return e.code;
+  } catch (const std::exception& e) {
+    g_create_error = e.what();
+    return HIP_ERROR;
+  }
+}
+
+void splat_destroy(splat_ctx* ctx) {
+  if (!ctx) return;
+  delete C(ctx);
+}
+
+const char* splat_last_error(const splat_ctx* ctx) {
+  if (!ctx) return g_create_error.c_str();
+  return reinterpret_cast<const Context*>(ctx)->last_error.c_str();
+}
+
+void* splat_stream(splat_ctx* ctx) { return ctx ? static_cast<void*>(C(ctx)->stream) : nullptr; }
+
+int splat_synchronize(splat_ctx* ctx) {
+  return guard(C(ctx), [&] { SPLAT_HIP(hipStreamSynchronize(C(ctx)->stream)); });
+}
+
+int splat_set_graphs(splat_ctx* ctx, int enable) {
+  return guard(C(ctx), [&] {
+    C(ctx)->graphs = enable != 0;
+    if (!enable) C(ctx)->clear_graphs();
+  });
+}
+
+int splat_set_debug_taps(splat_ctx* ctx, splat_tap_fn fn, void* user) {
+  return guard(C(ctx), [&] {
+    C(ctx)->hooks.tap = fn;
+    C(ctx)->hooks.tap_user = user;
+  });
+}
+
+int splat_load_da3(splat_ctx* ctx, const char* path, int variant, int dtype, int ref_strategy) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(path != nullptr, BAD_ARGUMENT, "path is NULL");
+    SafeTensors st;
+    st.open_file(path);
+    load_da3(C(ctx), st, variant, dtype, ref_strategy);
+  });
+}
+
+int splat_load_da3_bytes(splat_ctx* ctx, const uint8_t* bytes, size_t len, int variant, int dtype, int ref_strategy) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(bytes != nullptr, BAD_ARGUMENT, "bytes is NULL");
+    SafeTensors st;
+    st.open_bytes(bytes, len);
+    load_da3(C(ctx), st, variant, dtype, ref_strategy);
+  });
+}
+
+int splat_da3_forward_raw_device(splat_ctx* ctx, const float* images, int V, int H, int W, splat_da3_out* out,
+                                 int32_t* ref_view_device) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(out != nullptr, BAD_ARGUMENT, "out is NULL");
+    da3_device(C(ctx), images, V, H, W, *out, ref_view_device);
+  });
+}
+
+int splat_da3_forward_raw(splat_ctx* ctx, const float* images, int V, int H, int W, splat_progress_fn progress,
+                          void* user, splat_da3_out* out) {
+  Context* c = C(ctx);
+  int rc = guard(c, [&] {
+    SPLAT_CHECK(out != nullptr, BAD_ARGUMENT, "out is NULL");
+    check_images(images, V, H, W);
+    SPLAT_CHECK(c->da3 != nullptr, NOT_LOADED, "no Depth Anything 3 model loaded");
+    const size_t R = H / 14, Cc = W / 14, hw = size_t(H) * W, d = c->da3->dim();
+    const size_t img = size_t(V) * 3 * hw;
+    float* d_img = static_cast<float*>(staging(c, 0, img * 4));
+    splat_da3_out dev{};
+    dev.depth = static_cast<float*>(staging(c, 1, V * hw * 4));
+    dev.depth_conf = static_cast<float*>(staging(c, 2, V * hw * 4));
+    dev.ray_logits = out->ray_logits ? static_cast<float*>(staging(c, 3, V * 7 * 64 * R * Cc * 4)) : nullptr;
+    dev.pose_encoding = static_cast<float*>(staging(c, 4, V * 9 * 4));
+    dev.camera_tokens = out->camera_tokens ? static_cast<float*>(staging(c, 5, V * 2 * d * 4)) : nullptr;
+    int32_t* d_ref = static_cast<int32_t*>(staging(c, 6, 4));
+    SPLAT_HIP(hipMemcpyAsync(d_img, images, img * 4, hipMemcpyHostToDevice, c->stream));
+    c->hooks.progress = progress;
+    c->hooks.progress_user = user;
+    try {
+      da3_device(c, d_img, V, H, W, dev, d_ref);
+    } catch (...) {
+      c->hooks.progress = nullptr;
+      throw;
+    }
+    c->hooks.progress = nullptr;
+    SPLAT_CHECK(out->depth && out->depth_conf && out->pose_encoding, BAD_ARGUMENT, "missing output buffers");
+    d2h(c, out->depth, dev.depth, V * hw);
+    d2h(c, out->depth_conf, dev.depth_conf, V * hw);
+    d2h(c, out->ray_logits, dev.ray_logits, V * 7 * 64 * R * Cc);
+    d2h(c, out->pose_encoding, dev.pose_encoding, V * 9);
+    d2h(c, out->camera_tokens, dev.camera_tokens, V * 2 * d);
+    int32_t ref = 0;
+    SPLAT_HIP(hipMemcpyAsync(&ref, d_ref, 4, hipMemcpyDeviceToHost, c->stream));
+    SPLAT_HIP(hipStreamSynchronize(c->stream));
+    out->reference_view = ref;
+  });
+  if (rc != OK) return rc;
+  // depthanything3-rs/src/model.rs:139-146: finite and positive depth, finite confidence
+  for (size_t i = 0; i < size_t(V) * H * W; ++i) {
+    if (!std::isfinite(out->depth[i]) || !(out->depth[i] > 0.f) || !std::isfinite(out->depth_conf[i])) {
+      c->last_error = "view " + std::to_string(i / (size_t(H) * W)) + ": depth or confidence is not finite and positive";
+      return NONFINITE;
+    }
+  }
+  return OK;
+}
+
+void splat_ma_reference_spec(splat_ma_spec* s) {
+  if (!s) return;
+  // mapanything-rs/src/dinov2.rs:8-10, vit_block.rs:42-44, info_sharing.rs:12-14, dpt.rs:10-14, heads.rs:9-15
+  *s = splat_ma_spec{1536, 24, 24, 1, 4096, 1536, 24, 16, 1, 4096, {7, 11, 15}, {96, 192, 384, 768}, 256, 784, 196};
+}
+
+int splat_load_mapanything(splat_ctx* ctx, const char* path, const splat_ma_spec* spec, int dtype) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(path != nullptr, BAD_ARGUMENT, "path is NULL");
+    SafeTensors st;
+    st.open_file(path);
+    load_ma(C(ctx), st, spec, dtype);
+  });
+}
+
+int splat_load_mapanything_bytes(splat_ctx* ctx, const uint8_t* bytes, size_t len, const splat_ma_spec* spec, int dtype) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(bytes != nullptr, BAD_ARGUMENT, "bytes is NULL");
+    SafeTensors st;
+    st.open_bytes(bytes, len);
+    load_ma(C(ctx), st, spec, dtype);
+  });
+}
+
+int splat_ma_forward_device(splat_ctx* ctx, const float* images, int V, int H, int W, splat_ma_out* out) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(out != nullptr, BAD_ARGUMENT, "out is NULL");
+    ma_device(C(ctx), images, V, H, W, *out, nullptr, false);
+  });
+}
+
+int splat_ma_forward(splat_ctx* ctx, const float* images, int V, int H, int W, const double* intrinsics,
+                     splat_ma_out* out) {
+  Context* c = C(ctx);
+  return guard(c, [&] {
+    SPLAT_CHECK(out != nullptr, BAD_ARGUMENT, "out is NULL");
+    SPLAT_CHECK(intrinsics == nullptr, BAD_ARGUMENT, "known intrinsics (the ray encoder) are not supported");
+    check_images(images, V, H, W);
+    SPLAT_CHECK(c->ma != nullptr, NOT_LOADED, "no MapAnything model loaded");
+    const size_t hw = size_t(H) * W, img = size_t(V) * 3 * hw;
+    float* d_img = static_cast<float*>(staging(c, 10, img * 4));
+    splat_ma_out dev{};
+    dev.raw = out->raw ? static_cast<float*>(staging(c, 11, V * 6 * hw * 4)) : nullptr;
+    dev.quaternion = static_cast<float*>(staging(c, 12, V * 4 * 4));
+    dev.translation = static_cast<float*>(staging(c, 13, V * 3 * 4));
+    dev.scale = static_cast<float*>(staging(c, 14, 4));
+    dev.points = out->points ? static_cast<float*>(staging(c, 15, V * hw * 3 * 4)) : nullptr;
+    dev.conf = out->conf ? static_cast<float*>(staging(c, 16, V * hw * 4)) : nullptr;
+    dev.mask = out->mask ? static_cast<uint8_t*>(staging(c, 17, V * hw)) : nullptr;
+    SPLAT_HIP(hipMemcpyAsync(d_img, images, img * 4, hipMemcpyHostToDevice, c->stream));
+    ma_device(c, d_img, V, H, W, dev, nullptr, false);
+    d2h(c, out->raw, dev.raw, V * 6 * hw);
+    d2h(c, out->quaternion, dev.quaternion, V * 4);
+    d2h(c, out->translation, dev.translation, V * 3);
+    d2h(c, out->scale, dev.scale, 1);
+    d2h(c, out->points, dev.points, V * hw * 3);
+    d2h(c, out->conf, dev.conf, V * hw);
+    d2h(c, out->mask, dev.mask, V * hw);
+    SPLAT_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int splat_ma_encode_device(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(tokens != nullptr, BAD_ARGUMENT, "tokens is NULL");
+    splat_ma_out none{};
+    ma_device(C(ctx), images, V, H, W, none, tokens, true);
+  });
+}
+
+int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, const void* W, int N, int ldw,
+                      const float* bias, int act, void* out, int out_f32) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
+    SPLAT_CHECK(act >= 0 && act <= 2, BAD_ARGUMENT, "act");
+    GemmArgs g;
+    g.dt = dtype == SPLAT_F32 ? F32 : BF16;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.A = A;
+    g.lda = K;
+    g.W = W;
+    g.ldw = ldw;
+    g.bias = bias;
+    g.act = act;
+    g.out = out;
+    g.ldc = N;
+    g.out_f32 = out_f32;
+    gemm(C(ctx)->ex, g);
+  });
+}
+
+int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
+    AttnArgs a;
+    a.dt = dtype == SPLAT_F32 ? F32 : BF16;
+    const size_t es = dtype_size(a.dt);
+    a.q = qkv;
+    a.k = static_cast<const char*>(qkv) + size_t(heads) * 64 * es;
+    a.v = static_cast<const char*>(qkv) + size_t(heads) * 128 * es;
+    a.ld = 3L * heads * 64;
+    a.o = out;
+    a.ldo = long(heads) * 64;
+    a.L = L;
+    a.heads = heads;
+    a.seqs = S;
+    a.seq_stride = L;
+    attention(C(ctx)->ex, a);
+  });
+}
+
+int splat_ma_encode(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens) {
+  Context* c = C(ctx);
+  return guard(c, [&] {
+    SPLAT_CHECK(tokens != nullptr, BAD_ARGUMENT, "tokens is NULL");
+    check_images(images, V, H, W);
+    SPLAT_CHECK(c->ma != nullptr, NOT_LOADED, "no MapAnything model loaded");
+    const size_t hw = size_t(H) * W, img = size_t(V) * 3 * hw;
+    const size_t nt = size_t(V) * (1 + (H / 14) * (W / 14)) * c->ma->spec().enc_dim;
+    float* d_img = static_cast<float*>(staging(c, 20, img * 4));
+    float* d_tok = static_cast<float*>(staging(c, 21, nt * 4));
+    SPLAT_HIP(hipMemcpyAsync(d_img, images, img * 4, hipMemcpyHostToDevice, c->stream));
+    splat_ma_out none{};
+    ma_device(c, d_img, V, H, W, none, d_tok, true);
+    d2h(c, tokens, d_tok, nt);
+    SPLAT_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,75 @@
+// Shared device/host helpers for the splathip library (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+#include <stdexcept>
+#include <string>
+
+namespace splat {
+
+using bf16 = uint16_t;  // bfloat16 storage
+
+// --- errors -------------------------------------------------------------------------------
+
+enum Status {
+  OK = 0, BAD_ARGUMENT = 1, BAD_SHAPE = 2, MISSING_KEY = 3, SHAPE_MISMATCH = 4,
+  HIP_ERROR = 5, NONFINITE = 6, IO_ERROR = 7, NOT_LOADED = 8
+};
+
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define SPLAT_HIP(expr)                                                                   \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      throw ::splat::Error(::splat::HIP_ERROR, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+#define SPLAT_CHECK(cond, code, msg)                                                      \
+  do {                                                                                     \
+    if (!(cond)) throw ::splat::Error((code), (msg));                                     \
+  } while (0)
+
+// --- bf16 conversion ----------------------------------------------------------------------
+
+__host__ __device__ inline float bf2f(bf16 v) {
+  uint32_t u = uint32_t(v) << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+// Round to nearest even (NaN kept quiet).
+__host__ __device__ inline bf16 f2bf(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return bf16((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bf16(u >> 16);
+}
+
+template <typename T> __host__ __device__ inline float to_f(T v);
+template <> __host__ __device__ inline float to_f<float>(float v) { return v; }
+template <> __host__ __device__ inline float to_f<bf16>(bf16 v) { return bf2f(v); }
+
+template <typename T> __host__ __device__ inline T from_f(float v);
+template <> __host__ __device__ inline float from_f<float>(float v) { return v; }
+template <> __host__ __device__ inline bf16 from_f<bf16>(float v) { return f2bf(v); }
+
+// --- execution context for launches -------------------------------------------------------
+
+// Every launcher receives an Exec. With `dry` set, launchers only validate their arguments
+// and return: the forward runs once that way to size the activation arena.
+struct Exec {
+  hipStream_t stream = nullptr;
+  bool dry = false;
+};
+
+inline int cdiv(long a, long b) { return int((a + b - 1) / b); }
+
+}  // namespace splat

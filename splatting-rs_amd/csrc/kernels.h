@@ -1,0 +1,123 @@
+// Host-side launchers of the splathip HIP kernels. All tensors are device pointers; all
+// activations are row-major token matrices [rows, channels] or NHWC feature maps
+// [views, rows, cols, channels] (a token matrix of a patch grid IS its NHWC map).
+#pragma once
+
+#include "common.h"
+
+namespace splat {
+
+enum Dtype { F32 = 0, BF16 = 1 };
+inline size_t dtype_size(int dt) { return dt == F32 ? 4 : 2; }
+
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
+enum AMode { A_ROWS = 0, A_CONV = 1 };
+enum StoreMode { STORE_ROWS = 0, STORE_CONVT = 1 };
+
+// C[m, n] = epilogue(sum_k A[m, k] * W[n, k]).
+//
+// A (dtype `dt`): A_ROWS -> row-major [M, lda]; A_CONV -> implicit im2col of an NHWC map
+// [V, Hi, Wi, Cin] for a ks x ks convolution (stride, pad), k = (ky*ks + kx)*Cin + ci.
+// W (dtype `dt`): [N, ldw] row-major; columns K..ldw-1 must be zero and ldw a multiple of 64.
+// Epilogue, in this order: + bias[n]; activation; + addtab[(m % period) * N + n];
+// * gamma[n]; + res[row, n]; + res2[row, n]; store (`out_f32` selects fp32 or `dt`).
+// With rm_P > 0 the stored row is (m / rm_P) * rm_n + rm_off + m % rm_P (also for res/res2).
+// STORE_CONVT scatters a kernel=stride transposed convolution: m = (v, r, c) of an R x C
+// input grid, n = (dy*s + dx)*Cout + co -> out NHWC [V, R*s, C*s, Cout].
+struct GemmArgs {
+  int dt = BF16;
+  int M = 0, N = 0, K = 0;
+  const void* A = nullptr; long lda = 0;
+  int amode = A_ROWS;
+  int V = 0, Hi = 0, Wi = 0, Cin = 0, Ho = 0, Wo = 0, ks = 3, stride = 1, pad = 1;
+  int relu_in = 0;
+  const void* W = nullptr; long ldw = 0;
+  const float* bias = nullptr;
+  int act = ACT_NONE;
+  const float* addtab = nullptr; int addtab_period = 1;
+  const float* gamma = nullptr;
+  const void* res = nullptr; long ldres = 0; int res_f32 = 0;
+  const void* res2 = nullptr; long ldres2 = 0; int res2_f32 = 0;
+  void* out = nullptr; long ldc = 0; int out_f32 = 0;
+  int rm_P = 0, rm_n = 0, rm_off = 0;
+  int store = STORE_ROWS;
+  int ct_s = 1, ct_R = 0, ct_C = 0, ct_Cout = 0;
+};
+void gemm(const Exec& ex, const GemmArgs& a);
+
+// Flash attention, head dim 64, no mask: O = softmax(Q K^T / 8) V per (sequence, head).
+// Row t of sequence s is row s*seq_stride + t of q/k/v (row stride ld elements, head h at
+// column h*64); O rows likewise with stride ldo.
+struct AttnArgs {
+  int dt = BF16;
+  const void* q = nullptr; const void* k = nullptr; const void* v = nullptr; long ld = 0;
+  void* o = nullptr; long ldo = 0;
+  int L = 0, heads = 0, seqs = 1; long seq_stride = 0;
+};
+void attention(const Exec& ex, const AttnArgs& a);
+
+// LayerNorm over the last dim of rows: out[r] = LN(in[row_in(r)]) * w + b (w/b nullable);
+// row_in(r) = (r / rm_P) * rm_n + rm_off + r % rm_P when rm_P > 0, else r.
+void layer_norm(const Exec& ex, int in_dt, const void* in, long ldin, int out_dt, void* out, long ldout,
+                int rows, int n, const float* w, const float* b, float eps, int rm_P = 0, int rm_n = 0,
+                int rm_off = 0);
+
+// Per-head LayerNorm (64 ch, eps 1e-5) of q and k inside a [rows, 3*dim] qkv matrix, then 2D
+// RoPE. Token t's position: tok = t % n; tok 0 -> (0,0); patches -> (p/cols+1, p%cols+1)
+// (within a view) or (1,1) (across views). cs: [npos][16] cos then [npos][16] sin.
+void qk_norm_rope(const Exec& ex, int dt, void* qkv, int rows, int dim, const float* qw, const float* qb,
+                  const float* kw, const float* kb, int n, int cols, int across, const float* cs, int npos,
+                  int rope);
+
+// images fp32 [V,3,H,W] -> patch matrix [V*R*C, kpad] (dtype dt), k = c*196 + ky*14 + kx.
+void im2col_patch(const Exec& ex, int dt, const float* img, int V, int H, int W, void* out, int kpad);
+
+// xs[v*n + 0, :] = cls[:] + pos0[:] (fp32) for every view v.
+void write_class_rows(const Exec& ex, float* xs, int V, int n, int dim, const float* cls, const float* pos0);
+
+// Bilinear, align_corners=True, NHWC: sample grid computed for (Hf, Wf) outputs, the first
+// (Ho, Wo) of them written (crop). Optional + addtab[(oy*Wo+ox)*C + c] and relu.
+void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int Wi, int C, void* out, int Hf,
+                     int Wf, int Ho, int Wo, const float* addtab, int relu);
+
+// Pointwise output heads on an NHWC map [pix = V*H*W, Cin] (dt):
+//  PW_DEPTH: l = W x + b (2 ch) -> o0[pix] = exp(l0), o1[pix] = 1 + exp(l1)         (fp32)
+//  PW_RAY  : x' = relu(LN(x) no affine, eps 1e-5); o0 NCHW [V, Cout, H*W] = W x' + b   (fp32)
+//  PW_MA   : raw = W x + b (6 ch) -> o0 NCHW raw [V,6,H*W]; with scale (device scalar):
+//            points o1 [pix,3], conf o2 [pix], mask o3 (uint8) [pix]
+enum PwMode { PW_DEPTH = 0, PW_RAY = 1, PW_MA = 2 };
+void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, int hw, int cin, int cout,
+                    const float* w, const float* b, float* o0, float* o1, float* o2, uint8_t* o3,
+                    const float* scale);
+
+// y[m, n] = act(sum_k x[m*ldx + k] * W[n, k] + b[n]) for a handful of rows; x, y fp32,
+// W dtype wdt ([N, ldw]).
+void small_linear(const Exec& ex, int wdt, const float* x, long ldx, int M, int K, const void* W, long ldw,
+                  const float* b, float* y, long ldy, int N, int act);
+
+// DA3 reference-view choice on the device (saddle-balanced / first / middle) from the class
+// tokens xs[v*n, :dim] (fp32); writes the index to *ref.
+void select_reference_view(const Exec& ex, const float* xs, int V, int n, int dim, int strategy, int* ref);
+// xs[v*n] = cam[ref == v ? 0 : 1] (cam: [2, dim] fp32).
+void set_camera_tokens(const Exec& ex, float* xs, int V, int n, int dim, const float* cam, const int* ref);
+
+// DA3 hook: for every view and patch token t (1..n-1):
+//   h = cat(within[t], LN_{bn}(xs[t])) (2*dim), out[v*P + t-1] = LN_{hn}(h)  (dtype dt)
+// and when cam_out != null: cam_out[v] = cat(within[v*n], xs[v*n]) (fp32, no norm).
+void da3_hook(const Exec& ex, int dt, const float* within, const float* xs, int V, int n, int dim,
+              const float* bnw, const float* bnb, const float* hnw, const float* hnb, void* out, float* cam_out);
+
+// Generic elementwise helpers.
+void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count);
+void add_rows(const Exec& ex, float* xs, int rows, int dim, const float* vec);           // xs[r] += vec
+void copy_rows_f32(const Exec& ex, float* dst, long lddst, const float* src, long ldsrc, int rows, int dim);
+// gated[m, j] = silu(x12[m, j]) * x12[m, hidden + j]
+void swiglu_gate(const Exec& ex, int dt, const void* x12, int rows, int hidden, void* out);
+// mean over groups of P rows: out[g, c] = mean_p in[g*P + p, c] (fp32 out)
+void mean_rows(const Exec& ex, int dt, const void* in, int groups, int P, int C, float* out);
+// MA scale head tail + pose quaternion normalisation happen in small kernels:
+void exp_clamp(const Exec& ex, float* x, int count, float lo);
+void normalize_rows(const Exec& ex, float* x, int rows, int dim, float min_norm);
+void scale_rows(const Exec& ex, const float* x, int rows, int dim, const float* scale, float* out);
+
+}  // namespace splat

@@ -1,0 +1,571 @@
+// HBM-bound and small kernels around the GEMMs and attention: LayerNorms, qk-norm + 2D RoPE,
+// patch im2col, bilinear resize (align_corners=True), DPT output heads, small head linears,
+// DA3 reference-view selection and hook assembly, and elementwise helpers.
+#include "kernels.h"
+
+namespace splat {
+
+namespace {
+
+template <typename T> __device__ inline float ld(const void* p, long i) { return to_f<T>(reinterpret_cast<const T*>(p)[i]); }
+template <typename T> __device__ inline void st(void* p, long i, float v) { reinterpret_cast<T*>(p)[i] = from_f<T>(v); }
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+inline int in_dt_ok(int dt) { return dt == F32 || dt == BF16; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------
+// LayerNorm over rows, one wave per row, two passes (mean, then centred variance) with the
+// row re-read from cache. Biased variance and eps inside the sqrt, as torch/candle.
+template <typename TI, typename TO>
+__global__ void ln_kernel(const void* in, long ldin, void* out, long ldout, int rows, int n, const float* w,
+                          const float* b, float eps, int rmP, int rmn, int rmoff) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+  if (wave >= rows) return;
+  const long rin = rmP ? (long)(wave / rmP) * rmn + rmoff + wave % rmP : wave;
+  const long ib = rin * ldin, ob = (long)wave * ldout;
+  float s = 0.f;
+  for (int c = lane; c < n; c += 64) s += ld<TI>(in, ib + c);
+  const float mean = wave_sum(s) / n;
+  float v = 0.f;
+  for (int c = lane; c < n; c += 64) {
+    const float d = ld<TI>(in, ib + c) - mean;
+    v += d * d;
+  }
+  const float rstd = rsqrtf(wave_sum(v) / n + eps);
+  for (int c = lane; c < n; c += 64) {
+    float y = (ld<TI>(in, ib + c) - mean) * rstd;
+    if (w) y = y * w[c] + b[c];
+    st<TO>(out, ob + c, y);
+  }
+}
+
+void layer_norm(const Exec& ex, int in_dt, const void* in, long ldin, int out_dt, void* out, long ldout, int rows,
+                int n, const float* w, const float* b, float eps, int rm_P, int rm_n, int rm_off) {
+  SPLAT_CHECK(in_dt_ok(in_dt) && in_dt_ok(out_dt) && rows >= 0 && n > 0, BAD_ARGUMENT, "layer_norm args");
+  SPLAT_CHECK((w == nullptr) == (b == nullptr), BAD_ARGUMENT, "layer_norm: weight and bias come together");
+  if (ex.dry || rows == 0) return;
+  dim3 grid(cdiv(rows, 4));
+#define LNL(TI, TO) hipLaunchKernelGGL((ln_kernel<TI, TO>), grid, dim3(256), 0, ex.stream, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off)
+  if (in_dt == F32 && out_dt == F32) LNL(float, float);
+  else if (in_dt == F32 && out_dt == BF16) LNL(float, bf16);
+  else if (in_dt == BF16 && out_dt == F32) LNL(bf16, float);
+  else LNL(bf16, bf16);
+#undef LNL
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
+// qk-norm + RoPE (depthanything3-rs/src/vit_block.rs:149-158 and rope.rs:57-73): one thread
+// per (row, head, q|k), in place on the qkv matrix.
+template <typename T>
+__global__ void qk_kernel(void* qkv, int rows, int dim, const float* qw, const float* qb, const float* kw,
+                          const float* kb, int n, int cols, int across, const float* cs, int npos, int rope) {
+  const int heads = dim / 64;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)rows * heads * 2) return;
+  const int which = int(id & 1);
+  const long rh = id >> 1;
+  const long row = rh / heads;
+  const int h = int(rh - row * heads);
+  T* x = reinterpret_cast<T*>(qkv) + row * 3L * dim + which * dim + h * 64;
+  const float* w = which ? kw : qw;
+  const float* b = which ? kb : qb;
+  float v[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) v[i] = to_f<T>(x[i]);
+  if (w) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) s += v[i];
+    const float mean = s * (1.f / 64.f);
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const float d = v[i] - mean;
+      q += d * d;
+    }
+    const float rstd = rsqrtf(q * (1.f / 64.f) + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) v[i] = (v[i] - mean) * rstd * w[i] + b[i];
+  }
+  if (rope) {
+    const int tok = int(row % n);
+    int pr = 0, pc = 0;
+    if (tok > 0) {
+      if (across) { pr = 1; pc = 1; }
+      else { pr = (tok - 1) / cols + 1; pc = (tok - 1) % cols + 1; }
+    }
+#pragma unroll
+    for (int axis = 0; axis < 2; ++axis) {
+      const int pos = axis == 0 ? pr : pc;
+      const float* cosr = cs + (long)pos * 16;
+      const float* sinr = cs + (long)npos * 16 + (long)pos * 16;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float a = v[axis * 32 + i], bb = v[axis * 32 + 16 + i];
+        const float co = cosr[i], si = sinr[i];
+        v[axis * 32 + i] = a * co - bb * si;
+        v[axis * 32 + 16 + i] = bb * co + a * si;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 64; ++i) x[i] = from_f<T>(v[i]);
+}
+
+void qk_norm_rope(const Exec& ex, int dt, void* qkv, int rows, int dim, const float* qw, const float* qb,
+                  const float* kw, const float* kb, int n, int cols, int across, const float* cs, int npos, int rope) {
+  SPLAT_CHECK(dim % 64 == 0 && n > 0 && cols > 0, BAD_ARGUMENT, "qk_norm_rope args");
+  SPLAT_CHECK(!rope || cs != nullptr, BAD_ARGUMENT, "qk_norm_rope: missing rope table");
+  if (rope && !across) SPLAT_CHECK((n - 1) / cols + 1 < npos && cols + 1 <= npos, BAD_ARGUMENT, "rope table too small");
+  if (ex.dry || rows == 0) return;
+  const long threads = (long)rows * (dim / 64) * 2;
+  dim3 grid(cdiv(threads, 256));
+  if (dt == F32) hipLaunchKernelGGL(qk_kernel<float>, grid, dim3(256), 0, ex.stream, qkv, rows, dim, qw, qb, kw, kb, n, cols, across, cs, npos, rope);
+  else hipLaunchKernelGGL(qk_kernel<bf16>, grid, dim3(256), 0, ex.stream, qkv, rows, dim, qw, qb, kw, kb, n, cols, across, cs, npos, rope);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__global__ void im2col_kernel(const float* img, int V, int H, int W, void* out, int kpad) {
+  const int R = H / 14, C = W / 14;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)V * R * C * kpad;
+  if (id >= total) return;
+  const int k = int(id % kpad);
+  const long pidx = id / kpad;
+  float v = 0.f;
+  if (k < 588) {
+    const int c = k / 196, rem = k % 196, ky = rem / 14, kx = rem % 14;
+    const long vv = pidx / (R * C);
+    const int pp = int(pidx % (R * C)), py = pp / C, px = pp % C;
+    v = img[((vv * 3 + c) * H + py * 14 + ky) * W + px * 14 + kx];
+  }
+  st<T>(out, id, v);
+}
+
+void im2col_patch(const Exec& ex, int dt, const float* img, int V, int H, int W, void* out, int kpad) {
+  SPLAT_CHECK(H % 14 == 0 && W % 14 == 0 && kpad >= 588, BAD_ARGUMENT, "im2col args");
+  if (ex.dry) return;
+  const long total = (long)V * (H / 14) * (W / 14) * kpad;
+  dim3 grid(cdiv(total, 256));
+  if (dt == F32) hipLaunchKernelGGL(im2col_kernel<float>, grid, dim3(256), 0, ex.stream, img, V, H, W, out, kpad);
+  else hipLaunchKernelGGL(im2col_kernel<bf16>, grid, dim3(256), 0, ex.stream, img, V, H, W, out, kpad);
+  SPLAT_HIP(hipGetLastError());
+}
+
+__global__ void class_rows_kernel(float* xs, int V, int n, int dim, const float* cls, const float* pos0) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)V * dim) return;
+  const int v = int(id / dim), c = int(id % dim);
+  xs[(long)v * n * dim + c] = cls[c] + (pos0 ? pos0[c] : 0.f);
+}
+
+void write_class_rows(const Exec& ex, float* xs, int V, int n, int dim, const float* cls, const float* pos0) {
+  if (ex.dry) return;
+  hipLaunchKernelGGL(class_rows_kernel, dim3(cdiv((long)V * dim, 256)), dim3(256), 0, ex.stream, xs, V, n, dim, cls, pos0);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
+// Bilinear resize, align_corners=True (torch upsample_bilinear2d semantics: source =
+// dst * (in-1)/(out-1) in fp32, lambdas from the fractional part), NHWC.
+template <typename T>
+__global__ void resize_kernel(const void* in, int V, int Hi, int Wi, int C, void* out, int Hf, int Wf, int Ho, int Wo,
+                              const float* addtab, int relu) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)V * Ho * Wo * C;
+  if (id >= total) return;
+  const int c = int(id % C);
+  long r = id / C;
+  const int ox = int(r % Wo);
+  r /= Wo;
+  const int oy = int(r % Ho);
+  const long v = r / Ho;
+  const float sh = Hf > 1 ? float(Hi - 1) / float(Hf - 1) : 0.f;
+  const float sw = Wf > 1 ? float(Wi - 1) / float(Wf - 1) : 0.f;
+  const float fy = sh * oy, fx = sw * ox;
+  const int y0 = int(fy), x0 = int(fx);
+  const int y1 = y0 + (y0 < Hi - 1 ? 1 : 0), x1 = x0 + (x0 < Wi - 1 ? 1 : 0);
+  const float ly = fy - y0, lx = fx - x0;
+  const long b = v * Hi * Wi;
+  const float a00 = ld<T>(in, ((b + (long)y0 * Wi + x0) * C) + c);
+  const float a01 = ld<T>(in, ((b + (long)y0 * Wi + x1) * C) + c);
+  const float a10 = ld<T>(in, ((b + (long)y1 * Wi + x0) * C) + c);
+  const float a11 = ld<T>(in, ((b + (long)y1 * Wi + x1) * C) + c);
+  float val = (1.f - ly) * ((1.f - lx) * a00 + lx * a01) + ly * ((1.f - lx) * a10 + lx * a11);
+  if (addtab) val += addtab[((long)oy * Wo + ox) * C + c];
+  if (relu) val = fmaxf(val, 0.f);
+  st<T>(out, id, val);
+}
+
+void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int Wi, int C, void* out, int Hf, int Wf,
+                     int Ho, int Wo, const float* addtab, int relu) {
+  SPLAT_CHECK(Ho <= Hf && Wo <= Wf && Hi > 0 && Wi > 0, BAD_ARGUMENT, "resize args");
+  if (ex.dry) return;
+  const long total = (long)V * Ho * Wo * C;
+  dim3 grid(cdiv(total, 256));
+  if (dt == F32) hipLaunchKernelGGL(resize_kernel<float>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+  else hipLaunchKernelGGL(resize_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
+// Output heads: one thread per pixel; weights (cout x cin fp32) staged in LDS.
+template <typename T>
+__global__ void pw_kernel(int mode, const void* in, long pix, int hw, int cin, int cout, const float* w, const float* b,
+                          float* o0, float* o1, float* o2, uint8_t* o3, const float* scale) {
+  __shared__ float sw[8 * 256];
+  __shared__ float sb[8];
+  for (int i = threadIdx.x; i < cout * cin; i += blockDim.x) sw[i] = w[i];
+  if (threadIdx.x < cout) sb[threadIdx.x] = b[threadIdx.x];
+  __syncthreads();
+  const long px = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (px >= pix) return;
+  const long base = px * cin;
+  float mean = 0.f, rstd = 1.f;
+  if (mode == PW_RAY) {
+    float s = 0.f;
+    for (int c = 0; c < cin; ++c) s += ld<T>(in, base + c);
+    mean = s / cin;
+    float q = 0.f;
+    for (int c = 0; c < cin; ++c) {
+      const float d = ld<T>(in, base + c) - mean;
+      q += d * d;
+    }
+    rstd = rsqrtf(q / cin + 1e-5f);
+  }
+  float acc[8];
+#pragma unroll
+  for (int o = 0; o < 8; ++o) acc[o] = o < cout ? sb[o] : 0.f;
+  for (int c = 0; c < cin; ++c) {
+    float x = ld<T>(in, base + c);
+    if (mode == PW_RAY) x = fmaxf((x - mean) * rstd, 0.f);
+#pragma unroll
+    for (int o = 0; o < 8; ++o)
+      if (o < cout) acc[o] += sw[o * cin + c] * x;
+  }
+  const long v = px / hw, q = px % hw;
+  if (mode == PW_DEPTH) {
+    o0[px] = expf(acc[0]);
+    o1[px] = 1.f + expf(acc[1]);
+  } else if (mode == PW_RAY) {
+    for (int o = 0; o < cout; ++o) o0[(v * cout + o) * hw + q] = acc[o];
+  } else {
+    if (o0)
+      for (int o = 0; o < cout; ++o) o0[(v * cout + o) * hw + q] = acc[o];
+    // mapanything-rs/src/model.rs:155-168
+    const float nrm = fmaxf(sqrtf(acc[0] * acc[0] + acc[1] * acc[1] + acc[2] * acc[2]), 1e-8f);
+    const float depth = expf(acc[3]) * (scale ? *scale : 1.f);
+    if (o1) {
+      o1[px * 3 + 0] = acc[0] / nrm * depth;
+      o1[px * 3 + 1] = acc[1] / nrm * depth;
+      o1[px * 3 + 2] = acc[2] / nrm * depth;
+    }
+    if (o2) o2[px] = 1.f + expf(acc[4]);
+    if (o3) o3[px] = acc[5] > 0.f ? 1 : 0;
+  }
+}
+
+void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, int hw, int cin, int cout,
+                    const float* w, const float* b, float* o0, float* o1, float* o2, uint8_t* o3, const float* scale) {
+  SPLAT_CHECK(cout <= 8 && cout * cin <= 8 * 256 && hw > 0, BAD_ARGUMENT, "pointwise_head sizes");
+  SPLAT_CHECK(mode != PW_DEPTH || cout == 2, BAD_ARGUMENT, "depth head has 2 channels");
+  SPLAT_CHECK(mode != PW_MA || cout == 6, BAD_ARGUMENT, "MapAnything head has 6 channels");
+  if (ex.dry || pix == 0) return;
+  dim3 grid(cdiv(pix, 256));
+  if (dt == F32) hipLaunchKernelGGL(pw_kernel<float>, grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale);
+  else hipLaunchKernelGGL(pw_kernel<bf16>, grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
+// Small linears for the heads: one wave per output column n, looping over the M rows.
+template <typename TW>
+__global__ void small_linear_kernel(const float* x, long ldx, int M, int K, const void* W, long ldw, const float* b,
+                                    float* y, long ldy, int N, int act) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+  if (wave >= N) return;
+  const long wb = (long)wave * ldw;
+  for (int m = 0; m < M; ++m) {
+    float s = 0.f;
+    for (int k = lane; k < K; k += 64) s += x[m * ldx + k] * ld<TW>(W, wb + k);
+    s = wave_sum(s);
+    if (lane == 0) {
+      float v = s + (b ? b[wave] : 0.f);
+      if (act == ACT_RELU) v = fmaxf(v, 0.f);
+      y[m * ldy + wave] = v;
+    }
+  }
+}
+
+void small_linear(const Exec& ex, int wdt, const float* x, long ldx, int M, int K, const void* W, long ldw,
+                  const float* b, float* y, long ldy, int N, int act) {
+  SPLAT_CHECK(ldw >= K && ldx >= K && ldy >= N, BAD_ARGUMENT, "small_linear strides");
+  if (ex.dry || M == 0) return;
+  dim3 grid(cdiv(N, 4));
+  if (wdt == F32) hipLaunchKernelGGL(small_linear_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+  else hipLaunchKernelGGL(small_linear_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
+// depthanything3-rs/src/reference_view.rs:38-80 on the device, in f64: Gram matrix and row
+// sums of the class tokens, then mean cosine similarity, norm and unbiased variance of the
+// unit token, each min-max scaled, balance = sum |x - 0.5|, first argmin.
+constexpr int REF_MAX_VIEWS = 64;
+
+__global__ void ref_view_kernel(const float* xs, int V, int n, int dim, int strategy, int* ref) {
+  __shared__ double gram[REF_MAX_VIEWS * REF_MAX_VIEWS];
+  __shared__ double rsum[REF_MAX_VIEWS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (V < 3 || strategy == 0) {
+    if (threadIdx.x == 0) *ref = 0;
+    return;
+  }
+  if (strategy == 1) {
+    if (threadIdx.x == 0) *ref = V / 2;
+    return;
+  }
+  for (int pq = wave; pq < V * V + V; pq += nw) {
+    double s = 0.0;
+    if (pq < V * V) {
+      const int i = pq / V, j = pq % V;
+      if (j < i) continue;
+      const float* a = xs + (long)i * n * dim;
+      const float* b = xs + (long)j * n * dim;
+      for (int c = lane; c < dim; c += 64) s += double(a[c]) * double(b[c]);
+      s = wave_sum_d(s);
+      if (lane == 0) { gram[i * V + j] = s; gram[j * V + i] = s; }
+    } else {
+      const int i = pq - V * V;
+      const float* a = xs + (long)i * n * dim;
+      for (int c = lane; c < dim; c += 64) s += double(a[c]);
+      s = wave_sum_d(s);
+      if (lane == 0) rsum[i] = s;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  double sim[REF_MAX_VIEWS], nrm[REF_MAX_VIEWS], var[REF_MAX_VIEWS];
+  for (int i = 0; i < V; ++i) nrm[i] = sqrt(gram[i * V + i]);
+  for (int i = 0; i < V; ++i) {
+    double s = 0.0;
+    for (int j = 0; j < V; ++j)
+      if (j != i) s += gram[i * V + j] / (nrm[i] * nrm[j]);
+    sim[i] = s / (V - 1);
+    const double mean = rsum[i] / nrm[i] / dim;
+    const double sq = gram[i * V + i] / (nrm[i] * nrm[i]);
+    var[i] = (sq - dim * mean * mean) / (dim - 1);
+  }
+  double* metrics[3] = {sim, nrm, var};
+  double bal[REF_MAX_VIEWS];
+  for (int i = 0; i < V; ++i) bal[i] = 0.0;
+  for (int k = 0; k < 3; ++k) {
+    double lo = INFINITY, hi = -INFINITY;
+    for (int i = 0; i < V; ++i) { lo = fmin(lo, metrics[k][i]); hi = fmax(hi, metrics[k][i]); }
+    for (int i = 0; i < V; ++i) bal[i] += fabs((metrics[k][i] - lo) / (hi - lo + 1e-8) - 0.5);
+  }
+  int best = 0;
+  for (int i = 1; i < V; ++i)
+    if (bal[i] < bal[best]) best = i;
+  *ref = best;
+}
+
+void select_reference_view(const Exec& ex, const float* xs, int V, int n, int dim, int strategy, int* ref) {
+  SPLAT_CHECK(V <= REF_MAX_VIEWS, BAD_SHAPE, "reference-view selection supports at most 64 views");
+  if (ex.dry) return;
+  hipLaunchKernelGGL(ref_view_kernel, dim3(1), dim3(256), 0, ex.stream, xs, V, n, dim, strategy, ref);
+  SPLAT_HIP(hipGetLastError());
+}
+
+__global__ void camera_tokens_kernel(float* xs, int V, int n, int dim, const float* cam, const int* ref) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)V * dim) return;
+  const int v = int(id / dim), c = int(id % dim);
+  xs[(long)v * n * dim + c] = cam[(v == *ref ? 0 : dim) + c];
+}
+
+void set_camera_tokens(const Exec& ex, float* xs, int V, int n, int dim, const float* cam, const int* ref) {
+  if (ex.dry) return;
+  hipLaunchKernelGGL(camera_tokens_kernel, dim3(cdiv((long)V * dim, 256)), dim3(256), 0, ex.stream, xs, V, n, dim, cam, ref);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
+// depthanything3-rs/src/backbone.rs:177-189 + the dense head's input norm (dpt.rs:277).
+template <typename T>
+__global__ void da3_hook_kernel(const float* within, const float* xs, int V, int n, int dim, const float* bnw,
+                                const float* bnb, const float* hnw, const float* hnb, void* out, float* cam_out) {
+  const long wave = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wave >= (long)V * n) return;
+  const int v = int(wave / n), t = int(wave % n);
+  const float* a = xs + wave * dim;
+  const float* w = within + wave * dim;
+  if (t == 0) {
+    if (cam_out)
+      for (int c = lane; c < dim; c += 64) {
+        cam_out[(long)v * 2 * dim + c] = w[c];
+        cam_out[(long)v * 2 * dim + dim + c] = a[c];
+      }
+    return;
+  }
+  // backbone norm of the current output (eps 1e-5)
+  float s = 0.f;
+  for (int c = lane; c < dim; c += 64) s += a[c];
+  const float am = wave_sum(s) / dim;
+  float q = 0.f;
+  for (int c = lane; c < dim; c += 64) { const float d = a[c] - am; q += d * d; }
+  const float ar = rsqrtf(wave_sum(q) / dim + 1e-5f);
+  // head norm over cat(within, normed) (eps 1e-5)
+  s = 0.f;
+  for (int c = lane; c < dim; c += 64) s += w[c] + ((a[c] - am) * ar * bnw[c] + bnb[c]);
+  const float hm = wave_sum(s) / (2 * dim);
+  q = 0.f;
+  for (int c = lane; c < dim; c += 64) {
+    const float d0 = w[c] - hm, d1 = (a[c] - am) * ar * bnw[c] + bnb[c] - hm;
+    q += d0 * d0 + d1 * d1;
+  }
+  const float hr = rsqrtf(wave_sum(q) / (2 * dim) + 1e-5f);
+  const long ob = ((long)v * (n - 1) + t - 1) * 2 * dim;
+  for (int c = lane; c < dim; c += 64) {
+    const float an = (a[c] - am) * ar * bnw[c] + bnb[c];
+    st<T>(out, ob + c, (w[c] - hm) * hr * hnw[c] + hnb[c]);
+    st<T>(out, ob + dim + c, (an - hm) * hr * hnw[dim + c] + hnb[dim + c]);
+  }
+}
+
+void da3_hook(const Exec& ex, int dt, const float* within, const float* xs, int V, int n, int dim, const float* bnw,
+              const float* bnb, const float* hnw, const float* hnb, void* out, float* cam_out) {
+  if (ex.dry) return;
+  dim3 grid(cdiv((long)V * n, 4));
+  if (dt == F32) hipLaunchKernelGGL(da3_hook_kernel<float>, grid, dim3(256), 0, ex.stream, within, xs, V, n, dim, bnw, bnb, hnw, hnb, out, cam_out);
+  else hipLaunchKernelGGL(da3_hook_kernel<bf16>, grid, dim3(256), 0, ex.stream, within, xs, V, n, dim, bnw, bnb, hnw, hnb, out, cam_out);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
+template <typename TI, typename TO>
+__global__ void convert_kernel(const void* in, void* out, long count) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id < count) st<TO>(out, id, ld<TI>(in, id));
+}
+
+void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count) {
+  if (ex.dry || count == 0) return;
+  dim3 grid(cdiv(count, 256));
+  if (in_dt == F32 && out_dt == BF16) hipLaunchKernelGGL((convert_kernel<float, bf16>), grid, dim3(256), 0, ex.stream, in, out, count);
+  else if (in_dt == BF16 && out_dt == F32) hipLaunchKernelGGL((convert_kernel<bf16, float>), grid, dim3(256), 0, ex.stream, in, out, count);
+  else if (in_dt == F32) hipLaunchKernelGGL((convert_kernel<float, float>), grid, dim3(256), 0, ex.stream, in, out, count);
+  else hipLaunchKernelGGL((convert_kernel<bf16, bf16>), grid, dim3(256), 0, ex.stream, in, out, count);
+  SPLAT_HIP(hipGetLastError());
+}
+
+__global__ void add_rows_kernel(float* xs, int rows, int dim, const float* vec) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id < (long)rows * dim) xs[id] += vec[id % dim];
+}
+
+void add_rows(const Exec& ex, float* xs, int rows, int dim, const float* vec) {
+  if (ex.dry || rows == 0) return;
+  hipLaunchKernelGGL(add_rows_kernel, dim3(cdiv((long)rows * dim, 256)), dim3(256), 0, ex.stream, xs, rows, dim, vec);
+  SPLAT_HIP(hipGetLastError());
+}
+
+__global__ void copy_rows_kernel(float* dst, long lddst, const float* src, long ldsrc, int rows, int dim) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)rows * dim) return;
+  const long r = id / dim, c = id % dim;
+  dst[r * lddst + c] = src[r * ldsrc + c];
+}
+
+void copy_rows_f32(const Exec& ex, float* dst, long lddst, const float* src, long ldsrc, int rows, int dim) {
+  if (ex.dry || rows == 0) return;
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(cdiv((long)rows * dim, 256)), dim3(256), 0, ex.stream, dst, lddst, src, ldsrc, rows, dim);
+  SPLAT_HIP(hipGetLastError());
+}
+
+template <typename T>
+__global__ void swiglu_kernel(const void* x12, int rows, int hidden, void* out) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)rows * hidden) return;
+  const long r = id / hidden, j = id % hidden;
+  const float a = ld<T>(x12, r * 2 * hidden + j), b = ld<T>(x12, r * 2 * hidden + hidden + j);
+  st<T>(out, id, a / (1.f + expf(-a)) * b);
+}
+
+void swiglu_gate(const Exec& ex, int dt, const void* x12, int rows, int hidden, void* out) {
+  if (ex.dry || rows == 0) return;
+  dim3 grid(cdiv((long)rows * hidden, 256));
+  if (dt == F32) hipLaunchKernelGGL(swiglu_kernel<float>, grid, dim3(256), 0, ex.stream, x12, rows, hidden, out);
+  else hipLaunchKernelGGL(swiglu_kernel<bf16>, grid, dim3(256), 0, ex.stream, x12, rows, hidden, out);
+  SPLAT_HIP(hipGetLastError());
+}
+
+template <typename T>
+__global__ void mean_rows_kernel(const void* in, int groups, int P, int C, float* out) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)groups * C) return;
+  const long gi = id / C, c = id % C;
+  float s = 0.f;
+  for (int p = 0; p < P; ++p) s += ld<T>(in, (gi * P + p) * C + c);
+  out[id] = s / P;
+}
+
+void mean_rows(const Exec& ex, int dt, const void* in, int groups, int P, int C, float* out) {
+  if (ex.dry) return;
+  dim3 grid(cdiv((long)groups * C, 256));
+  if (dt == F32) hipLaunchKernelGGL(mean_rows_kernel<float>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
+  else hipLaunchKernelGGL(mean_rows_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
+  SPLAT_HIP(hipGetLastError());
+}
+
+__global__ void exp_clamp_kernel(float* x, int count, float lo) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id < count) x[id] = fmaxf(expf(x[id]), lo);
+}
+void exp_clamp(const Exec& ex, float* x, int count, float lo) {
+  if (ex.dry) return;
+  hipLaunchKernelGGL(exp_clamp_kernel, dim3(cdiv(count, 256)), dim3(256), 0, ex.stream, x, count, lo);
+  SPLAT_HIP(hipGetLastError());
+}
+
+__global__ void normalize_rows_kernel(float* x, int rows, int dim, float min_norm) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float s = 0.f;
+  for (int c = 0; c < dim; ++c) s += x[r * dim + c] * x[r * dim + c];
+  const float nrm = fmaxf(sqrtf(s), min_norm);
+  for (int c = 0; c < dim; ++c) x[r * dim + c] /= nrm;
+}
+void normalize_rows(const Exec& ex, float* x, int rows, int dim, float min_norm) {
+  if (ex.dry) return;
+  hipLaunchKernelGGL(normalize_rows_kernel, dim3(cdiv(rows, 64)), dim3(64), 0, ex.stream, x, rows, dim, min_norm);
+  SPLAT_HIP(hipGetLastError());
+}
+
+__global__ void scale_rows_kernel(const float* x, int count, const float* scale, float* out) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id < count) out[id] = x[id] * *scale;
+}
+void scale_rows(const Exec& ex, const float* x, int rows, int dim, const float* scale, float* out) {
+  if (ex.dry) return;
+  hipLaunchKernelGGL(scale_rows_kernel, dim3(cdiv(rows * dim, 256)), dim3(256), 0, ex.stream, x, rows * dim, scale, out);
+  SPLAT_HIP(hipGetLastError());
+}
+
+}  // namespace splat

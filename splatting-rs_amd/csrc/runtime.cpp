@@ -1,0 +1,537 @@
+#include "runtime.h"
+
+#include <array>
+#include <cmath>
+#include <functional>
+#include <cstring>
+#include <thread>
+
+namespace splat {
+
+// --- device memory --------------------------------------------------------------------------
+
+DevicePool::~DevicePool() {
+  for (void* p : ptrs_) (void)hipFree(p);
+}
+
+void* DevicePool::alloc(size_t bytes) {
+  void* p = nullptr;
+  SPLAT_HIP(hipMalloc(&p, bytes ? bytes : 16));
+  ptrs_.push_back(p);
+  total_ += bytes;
+  return p;
+}
+
+void* DevicePool::upload(const void* host, size_t bytes) {
+  void* p = alloc(bytes);
+  SPLAT_HIP(hipMemcpy(p, host, bytes, hipMemcpyHostToDevice));
+  return p;
+}
+
+Arena::~Arena() {
+  if (base_) (void)hipFree(base_);
+}
+
+void Arena::begin(bool dry) {
+  dry_ = dry;
+  used_ = 0;
+  if (dry) peak_ = 0;
+}
+
+void* Arena::alloc(size_t bytes) {
+  const size_t off = used_;
+  used_ += (bytes + 255) & ~size_t(255);
+  if (dry_) {
+    peak_ = std::max(peak_, used_);
+    return reinterpret_cast<void*>(uintptr_t(0x100000) + off);
+  }
+  SPLAT_CHECK(used_ <= cap_, HIP_ERROR, "activation arena overflow");
+  return base_ + off;
+}
+
+bool Arena::reserve(size_t bytes) {
+  if (bytes <= cap_) return false;
+  SPLAT_HIP(hipDeviceSynchronize());
+  if (base_) SPLAT_HIP(hipFree(base_));
+  base_ = nullptr;
+  cap_ = 0;
+  const size_t want = bytes + bytes / 8;
+  SPLAT_HIP(hipMalloc(reinterpret_cast<void**>(&base_), want));
+  cap_ = want;
+  return true;
+}
+
+// --- weights -------------------------------------------------------------------------------
+
+namespace {
+
+void parallel_for(size_t n, const std::function<void(size_t, size_t)>& fn) {
+  const size_t threads = n > (1u << 20) ? std::min<size_t>(16, std::max(1u, std::thread::hardware_concurrency())) : 1;
+  if (threads <= 1) {
+    fn(0, n);
+    return;
+  }
+  std::vector<std::thread> pool;
+  const size_t chunk = (n + threads - 1) / threads;
+  for (size_t t = 0; t < threads; ++t) {
+    const size_t a = t * chunk, b = std::min(n, a + chunk);
+    if (a < b) pool.emplace_back(fn, a, b);
+  }
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+Lin Loader::pack(std::vector<float>& rows, int n, int k, float* bias, int dt) {
+  Lin l;
+  l.N = n;
+  l.K = k;
+  l.dt = dt;
+  l.ldw = ((k + 63) / 64) * 64;
+  l.b = bias;
+  const size_t total = size_t(n) * l.ldw;
+  if (dt == F32) {
+    std::vector<float> buf(total, 0.f);
+    parallel_for(size_t(n), [&](size_t a, size_t b) {
+      for (size_t r = a; r < b; ++r) std::memcpy(&buf[r * l.ldw], &rows[r * k], sizeof(float) * k);
+    });
+    l.w = ctx_.pool.upload(buf.data(), total * 4);
+  } else {
+    std::vector<bf16> buf(total, 0);
+    parallel_for(size_t(n), [&](size_t a, size_t b) {
+      for (size_t r = a; r < b; ++r)
+        for (int c = 0; c < k; ++c) buf[r * l.ldw + c] = f2bf(rows[r * size_t(k) + c]);
+    });
+    l.w = ctx_.pool.upload(buf.data(), total * 2);
+  }
+  return l;
+}
+
+std::vector<float> Loader::host(const std::string& name, const std::vector<int64_t>& shape) {
+  return st_.f32(pre_ + name, shape);
+}
+
+float* Loader::vec(const std::string& name, const std::vector<int64_t>& shape) {
+  auto h = host(name, shape);
+  return static_cast<float*>(ctx_.pool.upload(h.data(), h.size() * 4));
+}
+
+Lin Loader::linear(const std::string& name, int n_out, int n_in, bool bias, int dt) {
+  auto w = host(name + ".weight", {n_out, n_in});
+  float* b = bias ? vec(name + ".bias", {n_out}) : nullptr;
+  return pack(w, n_out, n_in, b, dt < 0 ? dt_ : dt);
+}
+
+Conv Loader::conv(const std::string& name, int cout, int cin, int ks, bool bias) {
+  auto w = host(name + ".weight", {cout, cin, ks, ks});
+  std::vector<float> r(w.size());
+  const int kk = ks * ks;
+  for (int o = 0; o < cout; ++o)
+    for (int c = 0; c < cin; ++c)
+      for (int t = 0; t < kk; ++t) r[(size_t(o) * kk + t) * cin + c] = w[(size_t(o) * cin + c) * kk + t];
+  Conv cv;
+  cv.cout = cout;
+  cv.cin = cin;
+  cv.ks = ks;
+  float* b = bias ? vec(name + ".bias", {cout}) : nullptr;
+  cv.lin = pack(r, cout, kk * cin, b, dt_);
+  return cv;
+}
+
+ConvT Loader::convt(const std::string& name, int cin, int cout, int s) {
+  auto w = host(name + ".weight", {cin, cout, s, s});
+  auto b = host(name + ".bias", {cout});
+  const int n = s * s * cout;
+  std::vector<float> r(size_t(n) * cin);
+  std::vector<float> bx(n);
+  for (int ci = 0; ci < cin; ++ci)
+    for (int co = 0; co < cout; ++co)
+      for (int t = 0; t < s * s; ++t) r[(size_t(t) * cout + co) * cin + ci] = w[(size_t(ci) * cout + co) * s * s + t];
+  for (int t = 0; t < s * s; ++t)
+    for (int co = 0; co < cout; ++co) bx[size_t(t) * cout + co] = b[co];
+  ConvT ct;
+  ct.cin = cin;
+  ct.cout = cout;
+  ct.s = s;
+  float* bd = static_cast<float*>(ctx_.pool.upload(bx.data(), bx.size() * 4));
+  ct.lin = pack(r, n, cin, bd, dt_);
+  return ct;
+}
+
+LN Loader::ln(const std::string& name, int n) {
+  LN l;
+  l.n = n;
+  l.w = vec(name + ".weight", {n});
+  l.b = vec(name + ".bias", {n});
+  return l;
+}
+
+Block Loader::block(const std::string& p, int dim, int hidden, bool swiglu, bool qk) {
+  Block b;
+  b.dim = dim;
+  b.heads = dim / 64;
+  b.hidden = hidden;
+  b.swiglu = swiglu;
+  b.qk = qk;
+  b.n1 = ln(p + ".norm1", dim);
+  b.qkv = linear(p + ".attn.qkv", 3 * dim, dim);
+  if (qk) {
+    b.qn = ln(p + ".attn.q_norm", 64);
+    b.kn = ln(p + ".attn.k_norm", 64);
+  }
+  b.proj = linear(p + ".attn.proj", dim, dim);
+  b.ls1 = vec(p + ".ls1.gamma", {dim});
+  b.n2 = ln(p + ".norm2", dim);
+  if (swiglu) {
+    b.fc1 = linear(p + ".mlp.w12", 2 * hidden, dim);
+    b.fc2 = linear(p + ".mlp.w3", dim, hidden);
+  } else {
+    b.fc1 = linear(p + ".mlp.fc1", hidden, dim);
+    b.fc2 = linear(p + ".mlp.fc2", dim, hidden);
+  }
+  b.ls2 = vec(p + ".ls2.gamma", {dim});
+  return b;
+}
+
+// --- transformer block ----------------------------------------------------------------------
+
+void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, int hidden, bool swiglu) {
+  const size_t es = dtype_size(dt);
+  s.h = ctx.arena.alloc(rows * dim * es);
+  s.qkv = ctx.arena.alloc(rows * 3 * dim * es);
+  s.att = ctx.arena.alloc(rows * dim * es);
+  s.mid = ctx.arena.alloc(rows * hidden * es);
+  s.x12 = swiglu ? ctx.arena.alloc(rows * 2 * hidden * es) : nullptr;
+}
+
+void block_forward(Context& ctx, const Block& b, int dt, const float* in, float* out, long rows, int seqs, int L,
+                   BlockScratch& s, int rope, int n, int cols, const float* rope_table, int npos) {
+  const Exec& ex = ctx.ex;
+  const int d = b.dim;
+  // norm1 -> qkv
+  layer_norm(ex, F32, in, d, dt, s.h, d, int(rows), d, b.n1.w, b.n1.b, 1e-6f);
+  GemmArgs g;
+  g.dt = dt;
+  g.M = int(rows);
+  g.N = 3 * d;
+  g.K = d;
+  g.A = s.h;
+  g.lda = d;
+  g.W = b.qkv.w;
+  g.ldw = b.qkv.ldw;
+  g.bias = b.qkv.b;
+  g.out = s.qkv;
+  g.ldc = 3 * d;
+  gemm(ex, g);
+  if (b.qk || rope)
+    qk_norm_rope(ex, dt, s.qkv, int(rows), d, b.qk ? b.qn.w : nullptr, b.qk ? b.qn.b : nullptr, b.qk ? b.kn.w : nullptr,
+                 b.qk ? b.kn.b : nullptr, n, cols, rope == 2, rope_table, npos, rope != 0);
+  // attention
+  AttnArgs a;
+  a.dt = dt;
+  const size_t es = dtype_size(dt);
+  a.q = s.qkv;
+  a.k = static_cast<char*>(s.qkv) + d * es;
+  a.v = static_cast<char*>(s.qkv) + 2 * d * es;
+  a.ld = 3 * d;
+  a.o = s.att;
+  a.ldo = d;
+  a.L = L;
+  a.heads = b.heads;
+  a.seqs = seqs;
+  a.seq_stride = L;
+  attention(ex, a);
+  // out = in + ls1 * proj(att)
+  GemmArgs p;
+  p.dt = dt;
+  p.M = int(rows);
+  p.N = d;
+  p.K = d;
+  p.A = s.att;
+  p.lda = d;
+  p.W = b.proj.w;
+  p.ldw = b.proj.ldw;
+  p.bias = b.proj.b;
+  p.gamma = b.ls1;
+  p.res = in;
+  p.ldres = d;
+  p.res_f32 = 1;
+  p.out = out;
+  p.ldc = d;
+  p.out_f32 = 1;
+  gemm(ex, p);
+  // out += ls2 * mlp(norm2(out))
+  layer_norm(ex, F32, out, d, dt, s.h, d, int(rows), d, b.n2.w, b.n2.b, 1e-6f);
+  GemmArgs f1;
+  f1.dt = dt;
+  f1.M = int(rows);
+  f1.K = d;
+  f1.A = s.h;
+  f1.lda = d;
+  f1.W = b.fc1.w;
+  f1.ldw = b.fc1.ldw;
+  f1.bias = b.fc1.b;
+  if (b.swiglu) {
+    f1.N = 2 * b.hidden;
+    f1.out = s.x12;
+    f1.ldc = 2 * b.hidden;
+    gemm(ex, f1);
+    swiglu_gate(ex, dt, s.x12, int(rows), b.hidden, s.mid);
+  } else {
+    f1.N = b.hidden;
+    f1.act = ACT_GELU;
+    f1.out = s.mid;
+    f1.ldc = b.hidden;
+    gemm(ex, f1);
+  }
+  GemmArgs f2;
+  f2.dt = dt;
+  f2.M = int(rows);
+  f2.N = d;
+  f2.K = b.hidden;
+  f2.A = s.mid;
+  f2.lda = b.hidden;
+  f2.W = b.fc2.w;
+  f2.ldw = b.fc2.ldw;
+  f2.bias = b.fc2.b;
+  f2.gamma = b.ls2;
+  f2.res = out;
+  f2.ldres = d;
+  f2.res_f32 = 1;
+  f2.out = out;
+  f2.ldc = d;
+  f2.out_f32 = 1;
+  gemm(ex, f2);
+}
+
+// --- DPT building blocks --------------------------------------------------------------------
+
+GemmArgs lin_args(const Lin& l, int dt, const void* in, long lda, int rows, void* out, long ldc) {
+  GemmArgs g;
+  g.dt = dt;
+  g.M = rows;
+  g.N = l.N;
+  g.K = l.K;
+  g.A = in;
+  g.lda = lda;
+  g.W = l.w;
+  g.ldw = l.ldw;
+  g.bias = l.b;
+  g.out = out;
+  g.ldc = ldc;
+  return g;
+}
+
+GemmArgs conv_args(const Conv& c, int dt, const void* in, int V, int Hi, int Wi, int stride, void* out) {
+  if (c.ks == 1 && stride == 1) return lin_args(c.lin, dt, in, c.cin, V * Hi * Wi, out, c.cout);
+  GemmArgs g = lin_args(c.lin, dt, in, 0, 0, out, c.cout);
+  const int pad = c.ks / 2;
+  g.amode = A_CONV;
+  g.V = V;
+  g.Hi = Hi;
+  g.Wi = Wi;
+  g.Cin = c.cin;
+  g.ks = c.ks;
+  g.stride = stride;
+  g.pad = pad;
+  g.Ho = (Hi + 2 * pad - c.ks) / stride + 1;
+  g.Wo = (Wi + 2 * pad - c.ks) / stride + 1;
+  g.M = V * g.Ho * g.Wo;
+  return g;
+}
+
+void fusion_block(Context& ctx, int dt, const FusionW& f, const void* x, const void* skip, int V, int h, int w,
+                  int oh_full, int ow_full, int oh, int ow, void* out) {
+  const Exec& ex = ctx.ex;
+  const int F = f.u2.c1.cin;
+  const size_t bytes = size_t(V) * h * w * F * dtype_size(dt);
+  const size_t mark = ctx.arena.mark();
+  const void* xs = x;
+  if (skip) {
+    // xs = x + RCU1(skip) = x + skip + conv2(relu(conv1(relu(skip))))
+    void* a = ctx.arena.alloc(bytes);
+    GemmArgs g1 = conv_args(f.u1.c1, dt, skip, V, h, w, 1, a);
+    g1.relu_in = 1;
+    g1.act = ACT_RELU;
+    gemm(ex, g1);
+    void* xs2 = ctx.arena.alloc(bytes);
+    GemmArgs g2 = conv_args(f.u1.c2, dt, a, V, h, w, 1, xs2);
+    g2.res = skip;
+    g2.ldres = F;
+    g2.res2 = x;
+    g2.ldres2 = F;
+    gemm(ex, g2);
+    xs = xs2;
+  }
+  void* a2 = ctx.arena.alloc(bytes);
+  GemmArgs g3 = conv_args(f.u2.c1, dt, xs, V, h, w, 1, a2);
+  g3.relu_in = 1;
+  g3.act = ACT_RELU;
+  gemm(ex, g3);
+  void* y = ctx.arena.alloc(bytes);
+  GemmArgs g4 = conv_args(f.u2.c2, dt, a2, V, h, w, 1, y);
+  g4.res = xs;
+  g4.ldres = F;
+  gemm(ex, g4);
+  void* up = ctx.arena.alloc(size_t(V) * oh * ow * F * dtype_size(dt));
+  resize_bilinear(ex, dt, y, V, h, w, F, up, oh_full, ow_full, oh, ow, nullptr, 0);
+  gemm(ex, lin_args(f.out, dt, up, F, V * oh * ow, out, F));
+  ctx.arena.release(mark);
+}
+
+FusionW load_fusion(Loader& L, const std::string& p, int F, bool skip) {
+  FusionW f;
+  f.skip = skip;
+  if (skip) {
+    f.u1.c1 = L.conv(p + ".resConfUnit1.conv1", F, F, 3);
+    f.u1.c2 = L.conv(p + ".resConfUnit1.conv2", F, F, 3);
+  }
+  f.u2.c1 = L.conv(p + ".resConfUnit2.conv1", F, F, 3);
+  f.u2.c2 = L.conv(p + ".resConfUnit2.conv2", F, F, 3);
+  f.out = L.conv(p + ".out_conv", F, F, 1).lin;
+  return f;
+}
+
+// --- host tables ---------------------------------------------------------------------------
+
+namespace {
+
+constexpr int TRAINED_GRID = 37;
+
+std::array<double, 4> bicubic_weights(double t) {
+  const double a = -0.75;
+  auto near = [a](double x) { return ((a + 2.0) * x - (a + 3.0)) * x * x + 1.0; };
+  auto far = [a](double x) { return ((a * x - 5.0 * a) * x + 8.0 * a) * x - 4.0 * a; };
+  return {far(t + 1.0), near(t), near(1.0 - t), far(2.0 - t)};
+}
+
+struct Taps {
+  int idx[4];
+  double w[4];
+};
+
+std::vector<Taps> bicubic_taps(int in, int out, double scale) {
+  std::vector<Taps> taps(out);
+  for (int o = 0; o < out; ++o) {
+    const double src = (o + 0.5) / scale - 0.5;
+    const double fl = std::floor(src);
+    auto w = bicubic_weights(src - fl);
+    for (int i = 0; i < 4; ++i) {
+      long v = long(fl) + i - 1;
+      taps[o].idx[i] = int(std::min<long>(std::max<long>(v, 0), in - 1));
+      taps[o].w[i] = w[i];
+    }
+  }
+  return taps;
+}
+
+}  // namespace
+
+// mapanything-rs/src/dinov2.rs:42-76 (separable bicubic, f64, columns then rows) applied as
+// depthanything3-rs/src/backbone.rs:94-112: class slot kept, scale (out + 0.1) / 37.
+std::vector<float> resize_pos_embed(const std::vector<float>& pos, int dim, int rows, int cols) {
+  const int G = TRAINED_GRID;
+  std::vector<float> out(size_t(1 + rows * cols) * dim);
+  std::memcpy(out.data(), pos.data(), sizeof(float) * dim);
+  if (rows == G && cols == G) {
+    std::memcpy(out.data(), pos.data(), sizeof(float) * out.size());
+    return out;
+  }
+  const float* grid = pos.data() + dim;
+  auto ct = bicubic_taps(G, cols, (cols + 0.1) / G);
+  std::vector<double> horiz(size_t(G) * cols * dim, 0.0);
+  for (int r = 0; r < G; ++r)
+    for (int oc = 0; oc < cols; ++oc) {
+      double* dst = &horiz[(size_t(r) * cols + oc) * dim];
+      for (int t = 0; t < 4; ++t) {
+        const float* src = grid + (size_t(r) * G + ct[oc].idx[t]) * dim;
+        for (int c = 0; c < dim; ++c) dst[c] += ct[oc].w[t] * double(src[c]);
+      }
+    }
+  auto rt = bicubic_taps(G, rows, (rows + 0.1) / G);
+  for (int orow = 0; orow < rows; ++orow)
+    for (int oc = 0; oc < cols; ++oc) {
+      float* dst = &out[(1 + size_t(orow) * cols + oc) * dim];
+      for (int c = 0; c < dim; ++c) {
+        double s = 0.0;
+        for (int t = 0; t < 4; ++t) s += rt[orow].w[t] * horiz[(size_t(rt[orow].idx[t]) * cols + oc) * dim + c];
+        dst[c] = float(s);
+      }
+    }
+  return out;
+}
+
+// depthanything3-rs/src/rope.rs:26-54: angle = pos * 100^(-p/16) in f64, stored f32.
+std::vector<float> rope_table(int npos) {
+  std::vector<float> t(size_t(2) * npos * 16);
+  for (int pos = 0; pos < npos; ++pos)
+    for (int p = 0; p < 16; ++p) {
+      const double ang = double(pos) * (1.0 / std::pow(100.0, double(p) / 16.0));
+      t[size_t(pos) * 16 + p] = float(std::cos(ang));
+      t[size_t(npos) * 16 + size_t(pos) * 16 + p] = float(std::sin(ang));
+    }
+  return t;
+}
+
+// depthanything3-rs/src/uv_embed.rs:14-53, laid out [pixel][channel].
+std::vector<float> uv_table(int channels, int rows, int cols, double aspect) {
+  const double diag = std::sqrt(aspect * aspect + 1.0);
+  const double span[2] = {aspect / diag, 1.0 / diag};
+  auto coord = [&](int i, int count, int axis) {
+    const double edge = span[axis] * (count - 1.0) / count;
+    return count == 1 ? -edge : -edge + 2.0 * edge * i / (count - 1.0);
+  };
+  const int half = channels / 2, q = half / 2;
+  std::vector<float> t(size_t(rows) * cols * channels);
+  for (int r = 0; r < rows; ++r)
+    for (int c = 0; c < cols; ++c) {
+      float* dst = &t[(size_t(r) * cols + c) * channels];
+      const double pos[2] = {coord(c, cols, 0), coord(r, rows, 1)};
+      for (int axis = 0; axis < 2; ++axis)
+        for (int k = 0; k < q; ++k) {
+          const double ang = pos[axis] / std::pow(100.0, double(k) / q);
+          dst[axis * half + k] = float(std::sin(ang)) * 0.1f;
+          dst[axis * half + q + k] = float(std::cos(ang)) * 0.1f;
+        }
+    }
+  return t;
+}
+
+// --- context ---------------------------------------------------------------------------------
+
+Context::Context(int dev) : device(dev) {
+  SPLAT_HIP(hipSetDevice(dev));
+  SPLAT_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  ex.stream = stream;
+}
+
+Context::~Context() {
+  (void)hipSetDevice(device);
+  if (stream) (void)hipStreamSynchronize(stream);
+  clear_graphs();
+  da3.reset();
+  ma.reset();
+  for (auto& kv : staging)
+    if (kv.second.first) (void)hipFree(kv.second.first);
+  if (stream) (void)hipStreamDestroy(stream);
+}
+
+void* Context::staging_buffer(int slot, size_t bytes) {
+  auto& s = staging[slot];
+  if (s.second < bytes) {
+    SPLAT_HIP(hipStreamSynchronize(stream));
+    if (s.first) SPLAT_HIP(hipFree(s.first));
+    s.first = nullptr;
+    s.second = 0;
+    SPLAT_HIP(hipMalloc(&s.first, bytes));
+    s.second = bytes;
+  }
+  return s.first;
+}
+
+void Context::clear_graphs() {
+  for (auto& kv : graph_cache) (void)hipGraphExecDestroy(kv.second);
+  graph_cache.clear();
+}
+
+}  // namespace splat

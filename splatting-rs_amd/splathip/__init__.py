@@ -1,0 +1,253 @@
+"""ctypes binding of libsplathip (include/splathip.h, include/splathip_kernels.h).
+
+The host-side mirror of the reference's entry points:
+  Da3.load(path, variant, dtype, strategy)  ~ depthanything3-rs/src/weights.rs:26-48 load_model
+  Da3.forward_raw(images)                   ~ depthanything3-rs/src/model.rs:101-123 forward_raw
+  MapAnything.load(path, spec, dtype)       ~ mapanything-rs/src/model.rs:69-81 MapAnything::new
+  MapAnything.forward(images)               ~ mapanything-rs/src/model.rs:86-144 forward
+Errors raise SplatError carrying the library's status code and message (the reference's
+Result errors / panics). The library is required: importing this module fails loudly when
+libsplathip.so is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional
+
+import numpy as np
+
+from . import specs
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libsplathip.so")
+
+OK, BAD_ARGUMENT, BAD_SHAPE, MISSING_KEY, SHAPE_MISMATCH, HIP_ERROR, NONFINITE, IO_ERROR, NOT_LOADED = range(9)
+F32, BF16, F16 = 0, 1, 2
+DTYPES = {"f32": F32, "fp32": F32, "bf16": BF16, "f16": F16}
+STAGE_BLOCK, STAGE_DENSE_HEAD, STAGE_CAMERA_HEAD = 0, 1, 2
+
+
+class SplatError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+class MaSpecC(C.Structure):
+    _fields_ = [("enc_dim", C.c_int), ("enc_heads", C.c_int), ("enc_depth", C.c_int), ("enc_ffn", C.c_int),
+                ("enc_hidden", C.c_int), ("info_dim", C.c_int), ("info_heads", C.c_int), ("info_depth", C.c_int),
+                ("info_ffn", C.c_int), ("info_hidden", C.c_int), ("hooks", C.c_int * 3), ("dpt_dims", C.c_int * 4),
+                ("dpt_features", C.c_int), ("pose_dim", C.c_int), ("scale_dim", C.c_int)]
+
+    @classmethod
+    def from_spec(cls, s: specs.MaSpec) -> "MaSpecC":
+        return cls(s.enc_dim, s.enc_heads, s.enc_depth, s.enc_ffn, s.enc_hidden, s.info_dim, s.info_heads,
+                   s.info_depth, s.info_ffn, s.info_hidden, (C.c_int * 3)(*s.hooks), (C.c_int * 4)(*s.dpt_dims),
+                   s.dpt_features, s.pose_dim, s.scale_dim)
+
+
+class Da3OutC(C.Structure):
+    _fields_ = [("depth", C.c_void_p), ("depth_conf", C.c_void_p), ("ray_logits", C.c_void_p),
+                ("pose_encoding", C.c_void_p), ("camera_tokens", C.c_void_p), ("reference_view", C.c_int32)]
+
+
+class MaOutC(C.Structure):
+    _fields_ = [("raw", C.c_void_p), ("quaternion", C.c_void_p), ("translation", C.c_void_p), ("scale", C.c_void_p),
+                ("points", C.c_void_p), ("conf", C.c_void_p), ("mask", C.c_void_p)]
+
+
+PROGRESS_FN = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_void_p)
+TAP_FN = C.CFUNCTYPE(None, C.c_int, C.POINTER(C.c_float), C.c_int, C.c_int, C.c_void_p)
+
+# Every symbol the two public headers declare, with its ctypes signature.
+SIGNATURES = {
+    "splat_create": (C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
+    "splat_destroy": (None, [C.c_void_p]),
+    "splat_last_error": (C.c_char_p, [C.c_void_p]),
+    "splat_stream": (C.c_void_p, [C.c_void_p]),
+    "splat_synchronize": (C.c_int, [C.c_void_p]),
+    "splat_set_graphs": (C.c_int, [C.c_void_p, C.c_int]),
+    "splat_set_debug_taps": (C.c_int, [C.c_void_p, TAP_FN, C.c_void_p]),
+    "splat_load_da3": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int, C.c_int, C.c_int]),
+    "splat_load_da3_bytes": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int]),
+    "splat_da3_forward_raw": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, PROGRESS_FN, C.c_void_p,
+                                        C.POINTER(Da3OutC)]),
+    "splat_da3_forward_raw_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(Da3OutC),
+                                               C.c_void_p]),
+    "splat_load_mapanything": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(MaSpecC), C.c_int]),
+    "splat_load_mapanything_bytes": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(MaSpecC), C.c_int]),
+    "splat_ma_reference_spec": (None, [C.POINTER(MaSpecC)]),
+    "splat_ma_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.POINTER(MaOutC)]),
+    "splat_ma_forward_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(MaOutC)]),
+    "splat_ma_encode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "splat_ma_encode_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "splat_kernel_gemm": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int,
+                                    C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
+    "splat_kernel_attention": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded library (RTLD_LOCAL), with every declared symbol typed."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `make -C splatting-rs_amd` "
+                              "(or __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return C.c_void_p(a.ctypes.data) if a is not None else C.c_void_p(0)
+
+
+class Context:
+    """One HIP stream + weights + activation arena on a device (splat_create)."""
+
+    def __init__(self, device: int = 0):
+        self._lib = lib()
+        h = C.c_void_p()
+        rc = self._lib.splat_create(device, C.byref(h))
+        if rc != OK:
+            raise SplatError(rc, self._lib.splat_last_error(None).decode())
+        self.handle = h
+        self._callbacks = []
+
+    def close(self):
+        if self.handle:
+            self._lib.splat_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, rc: int):
+        if rc != OK:
+            raise SplatError(rc, self._lib.splat_last_error(self.handle).decode())
+
+    @property
+    def stream(self) -> int:
+        return self._lib.splat_stream(self.handle)
+
+    def synchronize(self):
+        self.check(self._lib.splat_synchronize(self.handle))
+
+    def set_graphs(self, enable: bool):
+        self.check(self._lib.splat_set_graphs(self.handle, int(enable)))
+
+    def set_debug_taps(self, fn):
+        """fn(block, ndarray [rows, dim]) per block, or None."""
+        if fn is None:
+            self.check(self._lib.splat_set_debug_taps(self.handle, TAP_FN(), None))
+            return
+        def tap(block, ptr, rows, dim, user):
+            fn(block, np.ctypeslib.as_array(ptr, shape=(rows, dim)).copy())
+        cb = TAP_FN(tap)
+        self._callbacks.append(cb)
+        self.check(self._lib.splat_set_debug_taps(self.handle, cb, None))
+
+    # --- Depth Anything 3 -------------------------------------------------------------------
+    def load_da3(self, path: str, variant: str = "small", dtype: str = "f32", strategy: int = specs.REF_SADDLE):
+        self.check(self._lib.splat_load_da3(self.handle, path.encode(), specs.DA3_VARIANT_INDEX[variant],
+                                            DTYPES[dtype], strategy))
+        self.da3_spec = specs.DA3_VARIANTS[variant]
+
+    def load_da3_bytes(self, data: bytes, variant: str = "small", dtype: str = "f32", strategy: int = specs.REF_SADDLE):
+        buf = np.frombuffer(data, np.uint8)
+        self.check(self._lib.splat_load_da3_bytes(self.handle, _ptr(buf), buf.size, specs.DA3_VARIANT_INDEX[variant],
+                                                  DTYPES[dtype], strategy))
+        self.da3_spec = specs.DA3_VARIANTS[variant]
+
+    def da3_forward_raw(self, images: np.ndarray, progress=None, rays: bool = True, camera_tokens: bool = True,
+                        allow_nonfinite: bool = False) -> dict:
+        x = np.ascontiguousarray(images, np.float32)
+        V, _, H, W = x.shape
+        R, Cc = H // 14, W // 14
+        d = self.da3_spec.dim
+        out = {
+            "depth": np.empty((V, H, W), np.float32),
+            "depth_conf": np.empty((V, H, W), np.float32),
+            "ray_logits": np.empty((V, 7, 8 * R, 8 * Cc), np.float32) if rays else None,
+            "pose_encoding": np.empty((V, 9), np.float32),
+            "camera_tokens": np.empty((V, 2 * d), np.float32) if camera_tokens else None,
+        }
+        o = Da3OutC(*[_ptr(out[k]) for k in ("depth", "depth_conf", "ray_logits", "pose_encoding", "camera_tokens")], 0)
+        cb = PROGRESS_FN(lambda s, b, u: progress(s, b)) if progress else PROGRESS_FN()
+        rc = self._lib.splat_da3_forward_raw(self.handle, _ptr(x), V, H, W, cb, None, C.byref(o))
+        if not (allow_nonfinite and rc == NONFINITE):
+            self.check(rc)
+        out["reference_view"] = int(o.reference_view)
+        return out
+
+    def da3_forward_raw_device(self, images_ptr: int, V: int, H: int, W: int, outs: dict, ref_ptr: int = 0):
+        o = Da3OutC(*[C.c_void_p(outs.get(k) or 0) for k in
+                      ("depth", "depth_conf", "ray_logits", "pose_encoding", "camera_tokens")], 0)
+        self.check(self._lib.splat_da3_forward_raw_device(self.handle, C.c_void_p(images_ptr), V, H, W, C.byref(o),
+                                                          C.c_void_p(ref_ptr)))
+
+    # --- MapAnything ------------------------------------------------------------------------
+    def load_mapanything(self, path: str, spec: Optional[specs.MaSpec] = None, dtype: str = "bf16"):
+        cs = MaSpecC.from_spec(spec) if spec is not None else None
+        self.check(self._lib.splat_load_mapanything(self.handle, path.encode(), C.byref(cs) if cs else None,
+                                                    DTYPES[dtype]))
+        self.ma_spec = spec or specs.MA_SPECS["reference"]
+
+    def ma_forward(self, images: np.ndarray, raw: bool = True, dense: bool = True) -> dict:
+        x = np.ascontiguousarray(images, np.float32)
+        V, _, H, W = x.shape
+        out = {
+            "raw": np.empty((V, 6, H, W), np.float32) if raw else None,
+            "quaternion": np.empty((V, 4), np.float32),
+            "translation": np.empty((V, 3), np.float32),
+            "scale": np.empty((1,), np.float32),
+            "points": np.empty((V, H, W, 3), np.float32) if dense else None,
+            "conf": np.empty((V, H, W), np.float32) if dense else None,
+            "mask": np.empty((V, H, W), np.uint8) if dense else None,
+        }
+        o = MaOutC(*[_ptr(out[k]) for k in ("raw", "quaternion", "translation", "scale", "points", "conf", "mask")])
+        self.check(self._lib.splat_ma_forward(self.handle, _ptr(x), V, H, W, None, C.byref(o)))
+        return out
+
+    def ma_forward_device(self, images_ptr: int, V: int, H: int, W: int, outs: dict):
+        o = MaOutC(*[C.c_void_p(outs.get(k) or 0) for k in
+                     ("raw", "quaternion", "translation", "scale", "points", "conf", "mask")])
+        self.check(self._lib.splat_ma_forward_device(self.handle, C.c_void_p(images_ptr), V, H, W, C.byref(o)))
+
+    def ma_encode(self, images: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(images, np.float32)
+        V, _, H, W = x.shape
+        n = 1 + (H // 14) * (W // 14)
+        tok = np.empty((V, n, self.ma_spec.enc_dim), np.float32)
+        self.check(self._lib.splat_ma_encode(self.handle, _ptr(x), V, H, W, _ptr(tok)))
+        return tok
+
+    def ma_encode_device(self, images_ptr: int, V: int, H: int, W: int, tokens_ptr: int):
+        self.check(self._lib.splat_ma_encode_device(self.handle, C.c_void_p(images_ptr), V, H, W, C.c_void_p(tokens_ptr)))
+
+    # --- kernels ------------------------------------------------------------------------------
+    def kernel_gemm(self, dtype: int, A: int, M: int, K: int, W: int, N: int, ldw: int, bias: int, act: int,
+                    out: int, out_f32: bool):
+        self.check(self._lib.splat_kernel_gemm(self.handle, dtype, C.c_void_p(A), M, K, C.c_void_p(W), N, ldw,
+                                               C.c_void_p(bias), act, C.c_void_p(out), int(out_f32)))
+
+    def kernel_attention(self, dtype: int, qkv: int, out: int, S: int, L: int, heads: int):
+        self.check(self._lib.splat_kernel_attention(self.handle, dtype, C.c_void_p(qkv), C.c_void_p(out), S, L, heads))
+
+
+def reference_ma_spec() -> dict:
+    s = MaSpecC()
+    lib().splat_ma_reference_spec(C.byref(s))
+    return {name: (list(getattr(s, name)) if name in ("hooks", "dpt_dims") else getattr(s, name))
+            for name, _ in MaSpecC._fields_}

@@ -1,0 +1,170 @@
+"""Depth Anything 3 through the C ABI (splat_load_da3 + splat_da3_forward_raw) against the
+CPU oracle (oracle/da3.py) on identical seeded weights and images.
+
+Tolerances:
+  fp32: depth, confidence, ray logits and pose encoding within 1e-3 relative error, where the
+        relative error of raw logits is floored at 1% of the tensor's max (conftest.rel_err);
+  bf16: per-block cosine of the residual stream >= 0.999 and median |depth/ref - 1| <= 1e-2.
+LayerScale 1e-5 (the benchmark's) leaves every block close to the identity, so each case also
+runs with LayerScale 1.0, where the per-block comparison is meaningful.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import report, rel_err, cosine
+
+pytestmark = pytest.mark.gpu
+
+import splathip
+from splathip import specs, synth
+from oracle import da3 as O
+
+SPEC = specs.DA3_VARIANTS["small"]
+
+
+@pytest.fixture(scope="module")
+def da3_weights(weights_dir):
+    out = {}
+    for ls in (1e-5, 1.0):
+        w = synth.generate(synth.da3_shapes(SPEC), seed=11, layer_scale=ls)
+        path = os.path.join(str(weights_dir), f"da3_small_ls{ls}.safetensors")
+        synth.save(path, w)
+        out[ls] = (path, w)
+    return out
+
+
+def _run(ctx, path, dtype, images, strategy, taps=False):
+    ctx.load_da3(path, "small", dtype, strategy)
+    got_taps = []
+    ctx.set_debug_taps((lambda b, x: got_taps.append(x)) if taps else None)
+    try:
+        out = ctx.da3_forward_raw(images)
+    finally:
+        ctx.set_debug_taps(None)
+    return out, got_taps
+
+
+def _oracle(w, images, strategy, force=None):
+    taps = []
+    ref = O.forward_raw(w, SPEC, images, strategy, force_reference=force, taps=taps)
+    return ref, taps
+
+
+def _check_fp32(out, ref):
+    errs = {
+        "depth": rel_err(out["depth"], ref["depth"].numpy(), tau=0.0),
+        "depth_conf": rel_err(out["depth_conf"], ref["depth_conf"].numpy(), tau=0.0),
+        "ray_logits": rel_err(out["ray_logits"], ref["ray_logits"].numpy()),
+        "pose_encoding": rel_err(out["pose_encoding"], ref["pose_encoding"].numpy()),
+        "camera_tokens": rel_err(out["camera_tokens"], ref["camera_tokens"].numpy()),
+    }
+    report("da3.fp32.errs", **{k: f"{v:.2e}" for k, v in errs.items()})
+    for k, v in errs.items():
+        assert v < 1e-3, (k, v)
+    assert out["reference_view"] == ref["reference_view"]
+
+
+@pytest.mark.parametrize("ls", [1e-5, 1.0])
+def test_da3_tiny_fp32(ctx, da3_weights, ls):
+    path, w = da3_weights[ls]
+    images = synth.procedural_images(3, 56, 42, seed=5)
+    report("da3.tiny.fp32", ls=ls, views=3, hw="56x42")
+    out, taps = _run(ctx, path, "f32", images, specs.REF_SADDLE, taps=True)
+    ref, rtaps = _oracle(w, images, specs.REF_SADDLE)
+    _check_fp32(out, ref)
+    assert len(taps) == len(rtaps) == SPEC.depth
+    for i, (a, b) in enumerate(zip(taps, rtaps)):
+        c = cosine(a, b.reshape(a.shape).numpy())
+        assert c > 0.99999, (i, c)
+    assert np.all(out["depth"] > 0) and np.all(out["depth_conf"] > 1)
+
+
+@pytest.mark.parametrize("ls", [1e-5, 1.0])
+def test_da3_tiny_bf16(ctx, da3_weights, ls):
+    path, w = da3_weights[ls]
+    images = synth.procedural_images(3, 56, 42, seed=6)
+    report("da3.tiny.bf16", ls=ls)
+    out, taps = _run(ctx, path, "bf16", images, specs.REF_FIRST, taps=True)
+    ref, rtaps = _oracle(w, images, specs.REF_FIRST)
+    for i, (a, b) in enumerate(zip(taps, rtaps)):
+        c = cosine(a, b.reshape(a.shape).numpy())
+        report("da3.tiny.bf16.block", i=i, cos=f"{c:.6f}")
+        assert c >= 0.999, (i, c)
+    med = float(np.median(np.abs(out["depth"] / ref["depth"].numpy() - 1)))
+    report("da3.tiny.bf16.depth", median_rel=f"{med:.2e}")
+    assert med <= 1e-2
+    assert cosine(out["ray_logits"], ref["ray_logits"].numpy()) >= 0.999
+    assert cosine(out["pose_encoding"], ref["pose_encoding"].numpy()) >= 0.999
+
+
+def test_da3_reference_view_strategies(ctx, da3_weights):
+    """Selection (reference_view.rs:38-80) on well-separated class tokens (LayerScale 1), for
+    every strategy, with the oracle's choice and the outputs in input order."""
+    path, w = da3_weights[1.0]
+    images = synth.procedural_images(4, 42, 56, seed=9)
+    for strategy in (specs.REF_FIRST, specs.REF_MIDDLE, specs.REF_SADDLE):
+        report("da3.refview", strategy=strategy)
+        out, _ = _run(ctx, path, "f32", images, strategy)
+        ref, _ = _oracle(w, images, strategy)
+        assert out["reference_view"] == ref["reference_view"]
+        _check_fp32(out, ref)
+
+
+def test_da3_two_views_keep_first(ctx, da3_weights):
+    path, w = da3_weights[1.0]
+    images = synth.procedural_images(2, 42, 42, seed=10)
+    out, _ = _run(ctx, path, "f32", images, specs.REF_SADDLE)
+    assert out["reference_view"] == 0
+
+
+@pytest.mark.slow
+def test_da3_c1_fp32(ctx, da3_weights):
+    """1 view 504x504 fp32, uniform pixels, LayerScale 1e-5."""
+    path, w = da3_weights[1e-5]
+    images = synth.uniform_images(1, 504, 504, seed=1)
+    report("da3.C1.fp32")
+    out, _ = _run(ctx, path, "f32", images, specs.REF_SADDLE)
+    ref, _ = _oracle(w, images, specs.REF_SADDLE)
+    _check_fp32(out, ref)
+
+
+@pytest.mark.slow
+def test_da3_c2_bf16(ctx, da3_weights):
+    """6 views 378x504 bf16 (procedural images), LayerScale 1e-5; the
+    reference view is pinned to the oracle's choice (its near-tie is tested above)."""
+    path, w = da3_weights[1e-5]
+    images = synth.procedural_images(6, 378, 504, seed=2)
+    report("da3.C2.bf16")
+    out, _ = _run(ctx, path, "bf16", images, specs.REF_FIRST)
+    ref, _ = _oracle(w, images, specs.REF_FIRST)
+    med = float(np.median(np.abs(out["depth"] / ref["depth"].numpy() - 1)))
+    report("da3.C2.bf16.depth", median_rel=f"{med:.2e}")
+    assert med <= 1e-2
+    for key in ("depth", "depth_conf", "ray_logits", "pose_encoding"):
+        c = cosine(out[key] - np.mean(out[key]), ref[key].numpy() - np.mean(ref[key].numpy()))
+        report("da3.C2.bf16.cos", key=key, cos=f"{c:.6f}")
+        assert c >= 0.999, (key, c)
+
+
+def test_da3_errors(ctx, da3_weights, weights_dir):
+    path, w = da3_weights[1e-5]
+    ctx.load_da3(path, "small", "f32")
+    with pytest.raises(splathip.SplatError) as e:
+        ctx.da3_forward_raw(np.zeros((1, 3, 50, 42), np.float32))
+    assert e.value.code == splathip.BAD_SHAPE
+    w2 = dict(w)
+    del w2["model.head.scratch.output_conv2.2.bias"]
+    p2 = os.path.join(str(weights_dir), "da3_missing.safetensors")
+    synth.save(p2, w2)
+    with pytest.raises(splathip.SplatError) as e:
+        ctx.load_da3(p2, "small", "f32")
+    assert e.value.code == splathip.MISSING_KEY
+    w3 = dict(w)
+    w3["model.backbone.pretrained.norm.weight"] = np.ones(100, np.float32)
+    p3 = os.path.join(str(weights_dir), "da3_badshape.safetensors")
+    synth.save(p3, w3)
+    with pytest.raises(splathip.SplatError) as e:
+        ctx.load_da3(p3, "small", "f32")
+    assert e.value.code == splathip.SHAPE_MISMATCH

@@ -1,0 +1,127 @@
+"""MapAnything through the C ABI (splat_load_mapanything + splat_ma_forward / splat_ma_encode)
+against the CPU oracle (oracle/mapanything.py) on identical seeded weights and images, for
+small specs of the same topology (GELU and SwiGLU feed-forwards, with and without the
+encoder->info projection). Tolerances as in test_gpu_da3.py."""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import report, rel_err, cosine
+
+pytestmark = pytest.mark.gpu
+
+import splathip
+from splathip import specs, synth
+from oracle import mapanything as O
+
+
+@pytest.fixture(scope="module")
+def ma_weights(weights_dir):
+    out = {}
+    for name in ("tiny", "tiny_proj"):
+        for ls in (1e-5, 1.0):
+            spec = specs.MA_SPECS[name]
+            w = synth.generate(synth.ma_shapes(spec), seed=21, layer_scale=ls)
+            path = os.path.join(str(weights_dir), f"ma_{name}_{ls}.safetensors")
+            synth.save(path, w)
+            out[(name, ls)] = (path, w, spec)
+    return out
+
+
+def _check_fp32(out, ref):
+    errs = {
+        "raw": rel_err(out["raw"], ref["raw"].numpy()),
+        "quaternion": rel_err(out["quaternion"], ref["quaternion"].numpy()),
+        "translation": rel_err(out["translation"], ref["translation"].numpy()),
+        "scale": rel_err(out["scale"], [ref["scale"]], tau=0.0),
+        "points": rel_err(out["points"], ref["points"].permute(0, 2, 3, 1).numpy()),
+        "conf": rel_err(out["conf"], ref["conf"].numpy(), tau=0.0),
+    }
+    report("ma.fp32.errs", **{k: f"{v:.2e}" for k, v in errs.items()})
+    for k, v in errs.items():
+        assert v < 1e-3, (k, v)
+    agree = np.mean(out["mask"].astype(bool) == ref["mask"].numpy())
+    assert agree > 0.999
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_proj"])
+@pytest.mark.parametrize("ls", [1e-5, 1.0])
+def test_ma_tiny_fp32(ctx, ma_weights, name, ls):
+    path, w, spec = ma_weights[(name, ls)]
+    images = synth.procedural_images(3, 56, 70, seed=4)
+    report("ma.tiny.fp32", spec=name, ls=ls)
+    ctx.load_mapanything(path, spec, "f32")
+    taps = []
+    ctx.set_debug_taps(lambda b, x: taps.append(x))
+    try:
+        out = ctx.ma_forward(images)
+    finally:
+        ctx.set_debug_taps(None)
+    enc_taps, info_taps = [], []
+    ref = O.forward(w, spec, images, taps=enc_taps, info_taps=info_taps)
+    _check_fp32(out, ref)
+    rtaps = [t.reshape(-1, t.shape[-1]) for t in enc_taps + info_taps]
+    assert len(taps) == len(rtaps)
+    for i, (a, b) in enumerate(zip(taps, rtaps)):
+        assert cosine(a, b.numpy()) > 0.99999, i
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_proj"])
+def test_ma_tiny_bf16(ctx, ma_weights, name):
+    path, w, spec = ma_weights[(name, 1.0)]
+    images = synth.procedural_images(3, 56, 70, seed=8)
+    report("ma.tiny.bf16", spec=name)
+    ctx.load_mapanything(path, spec, "bf16")
+    taps = []
+    ctx.set_debug_taps(lambda b, x: taps.append(x))
+    try:
+        out = ctx.ma_forward(images)
+    finally:
+        ctx.set_debug_taps(None)
+    enc_taps, info_taps = [], []
+    ref = O.forward(w, spec, images, taps=enc_taps, info_taps=info_taps)
+    for i, (a, b) in enumerate(zip(taps, enc_taps + info_taps)):
+        c = cosine(a, b.reshape(a.shape).numpy())
+        assert c >= 0.999, (i, c)
+    depth = np.exp(out["raw"][:, 3]) * out["scale"][0]
+    rdepth = np.exp(ref["raw"][:, 3].numpy()) * ref["scale"]
+    med = float(np.median(np.abs(depth / rdepth - 1)))
+    report("ma.tiny.bf16.depth", median_rel=f"{med:.2e}")
+    assert med <= 1e-2
+    assert cosine(out["raw"], ref["raw"].numpy()) >= 0.999
+    assert cosine(out["quaternion"], ref["quaternion"].numpy()) >= 0.999
+
+
+def test_ma_encoder_only(ctx, ma_weights):
+    path, w, spec = ma_weights[("tiny", 1.0)]
+    images = synth.uniform_images(2, 42, 56, seed=3)
+    ctx.load_mapanything(path, spec, "f32")
+    tok = ctx.ma_encode(images)
+    ref = O.forward(w, spec, images, encoder_only=True)["encoder_tokens"].numpy()
+    assert rel_err(tok, ref) < 1e-3
+
+
+def test_ma_views_equivariance(ctx, ma_weights):
+    """Permuting views 1.. (view 0 carries the reference embedding) permutes every per-view
+    output and leaves the scale unchanged (global attention is permutation-equivariant)."""
+    path, w, spec = ma_weights[("tiny", 1.0)]
+    images = synth.procedural_images(4, 42, 42, seed=12)
+    ctx.load_mapanything(path, spec, "f32")
+    a = ctx.ma_forward(images)
+    perm = [0, 3, 1, 2]
+    b = ctx.ma_forward(images[perm])
+    assert rel_err(b["raw"], a["raw"][perm]) < 1e-4
+    assert rel_err(b["scale"], a["scale"], tau=0.0) < 1e-5
+
+
+def test_ma_errors(ctx, ma_weights):
+    path, w, spec = ma_weights[("tiny", 1e-5)]
+    ctx.load_mapanything(path, spec, "f32")
+    with pytest.raises(splathip.SplatError) as e:
+        ctx.ma_forward(np.zeros((1, 3, 56, 69), np.float32))
+    assert e.value.code == splathip.BAD_SHAPE
+    bad = specs.MA_SPECS["tiny_proj"]
+    with pytest.raises(splathip.SplatError) as e:
+        ctx.load_mapanything(path, bad, "f32")
+    assert e.value.code in (splathip.MISSING_KEY, splathip.SHAPE_MISMATCH)
