@@ -22,6 +22,24 @@ int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, co
  * reading q, k and v from a [S*L, 3*heads*64] qkv matrix (q | k | v column blocks). */
 int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads);
 
+/* Convolution (zero padding ks/2) on NHWC maps as an implicit GEMM:
+ * out[V, Ho, Wo, Cout] = act(conv(relu_in ? relu(in) : in, w) + bias) + res, with
+ * w [Cout, ldw] holding k = (ky*ks + kx)*Cin + ci (candle/PyTorch weight [Cout, Cin, ks, ks]
+ * permuted), ldw a multiple of 64 with zero columns past ks*ks*Cin; res NHWC like out or NULL. */
+int splat_kernel_conv2d(splat_ctx* ctx, int dtype, const void* in, int V, int H, int W, int Cin, const void* w,
+                        int Cout, int ldw, int ks, int stride, const float* bias, int relu_in, int act,
+                        const void* res, void* out);
+
+/* Transposed convolution with kernel == stride s on NHWC maps: out[V, R*s, C*s, Cout];
+ * w [s*s*Cout, ldw] with row (dy*s + dx)*Cout + co = weight[:, co, dy, dx] (PyTorch weight
+ * [Cin, Cout, s, s]); bias [s*s*Cout] (the Cout biases repeated per (dy, dx)). */
+int splat_kernel_conv_transpose2d(splat_ctx* ctx, int dtype, const void* in, int V, int R, int C, int Cin,
+                                  const void* w, int Cout, int ldw, int s, const float* bias, void* out);
+
+/* Bilinear resize with align_corners=True (torch upsample_bilinear2d) of NHWC maps. */
+int splat_kernel_resize_bilinear(splat_ctx* ctx, int dtype, const void* in, int V, int Hi, int Wi, int C, void* out,
+                                 int Ho, int Wo);
+
 #ifdef __cplusplus
 }
 #endif

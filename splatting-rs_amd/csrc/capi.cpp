@@ -328,6 +328,60 @@ int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out
   });
 }
 
+int splat_kernel_conv2d(splat_ctx* ctx, int dtype, const void* in, int V, int H, int W, int Cin, const void* w,
+                        int Cout, int ldw, int ks, int stride, const float* bias, int relu_in, int act,
+                        const void* res, void* out) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
+    SPLAT_CHECK(ks == 1 || ks == 3, BAD_ARGUMENT, "kernel size must be 1 or 3");
+    Conv c;
+    c.cout = Cout;
+    c.cin = Cin;
+    c.ks = ks;
+    c.lin.w = const_cast<void*>(w);
+    c.lin.ldw = ldw;
+    c.lin.N = Cout;
+    c.lin.K = ks * ks * Cin;
+    c.lin.b = const_cast<float*>(bias);
+    const int dt = dtype == SPLAT_F32 ? F32 : BF16;
+    GemmArgs g = conv_args(c, dt, in, V, H, W, stride, out);
+    g.relu_in = relu_in;
+    g.act = act;
+    g.res = res;
+    g.ldres = Cout;
+    gemm(C(ctx)->ex, g);
+  });
+}
+
+int splat_kernel_conv_transpose2d(splat_ctx* ctx, int dtype, const void* in, int V, int R, int Cc, int Cin,
+                                  const void* w, int Cout, int ldw, int s, const float* bias, void* out) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
+    Lin l;
+    l.w = const_cast<void*>(w);
+    l.ldw = ldw;
+    l.N = s * s * Cout;
+    l.K = Cin;
+    l.b = const_cast<float*>(bias);
+    GemmArgs u = lin_args(l, dtype == SPLAT_F32 ? F32 : BF16, in, Cin, V * R * Cc, out, 0);
+    u.store = STORE_CONVT;
+    u.V = V;
+    u.ct_s = s;
+    u.ct_R = R;
+    u.ct_C = Cc;
+    u.ct_Cout = Cout;
+    gemm(C(ctx)->ex, u);
+  });
+}
+
+int splat_kernel_resize_bilinear(splat_ctx* ctx, int dtype, const void* in, int V, int Hi, int Wi, int Cc, void* out,
+                                 int Ho, int Wo) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
+    resize_bilinear(C(ctx)->ex, dtype == SPLAT_F32 ? F32 : BF16, in, V, Hi, Wi, Cc, out, Ho, Wo, Ho, Wo, nullptr, 0);
+  });
+}
+
 int splat_ma_encode(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens) {
   Context* c = C(ctx);
   return guard(c, [&] {

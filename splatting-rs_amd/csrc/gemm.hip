@@ -52,8 +52,11 @@ template <> struct Mfma<float> {
 
 __device__ inline float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
 
-__device__ inline float load_any(const void* p, long i, int f32) {
-  return f32 ? reinterpret_cast<const float*>(p)[i] : bf2f(reinterpret_cast<const bf16*>(p)[i]);
+// A residual is fp32 when flagged, else stored in the kernel's own dtype T.
+template <typename T>
+__device__ inline float load_res(const void* p, long i, int f32) {
+  if (f32 || sizeof(T) == 4) return reinterpret_cast<const float*>(p)[i];
+  return bf2f(reinterpret_cast<const bf16*>(p)[i]);
 }
 
 constexpr int LDS_ROW = 144;  // bytes per tile row: 128 bytes of K + 16 bytes against bank conflicts
@@ -199,8 +202,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs p) {
         if (p.addtab) v += p.addtab[(m % p.addtab_period) * p.N + n];
         v *= gam;
         long row = p.rm_P ? (m / p.rm_P) * p.rm_n + p.rm_off + m % p.rm_P : m;
-        if (p.res) v += load_any(p.res, row * p.ldres + n, p.res_f32);
-        if (p.res2) v += load_any(p.res2, row * p.ldres2 + n, p.res2_f32);
+        if (p.res) v += load_res<T>(p.res, row * p.ldres + n, p.res_f32);
+        if (p.res2) v += load_res<T>(p.res2, row * p.ldres2 + n, p.res2_f32);
         long idx;
         if (p.store == STORE_CONVT) {
           const long hw = (long)p.ct_R * p.ct_C;

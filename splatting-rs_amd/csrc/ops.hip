@@ -195,12 +195,12 @@ __global__ void resize_kernel(const void* in, int V, int Hi, int Wi, int C, void
   r /= Wo;
   const int oy = int(r % Ho);
   const long v = r / Ho;
-  const float sh = Hf > 1 ? float(Hi - 1) / float(Hf - 1) : 0.f;
-  const float sw = Wf > 1 ? float(Wi - 1) / float(Wf - 1) : 0.f;
-  const float fy = sh * oy, fx = sw * ox;
-  const int y0 = int(fy), x0 = int(fx);
+  // Source coordinates in f64 (exact to well below an fp32 ulp), weights in fp32.
+  const double fy = Hf > 1 ? double(Hi - 1) * oy / double(Hf - 1) : 0.0;
+  const double fx = Wf > 1 ? double(Wi - 1) * ox / double(Wf - 1) : 0.0;
+  const int y0 = min(int(fy), Hi - 1), x0 = min(int(fx), Wi - 1);
   const int y1 = y0 + (y0 < Hi - 1 ? 1 : 0), x1 = x0 + (x0 < Wi - 1 ? 1 : 0);
-  const float ly = fy - y0, lx = fx - x0;
+  const float ly = float(fy - y0), lx = float(fx - x0);
   const long b = v * Hi * Wi;
   const float a00 = ld<T>(in, ((b + (long)y0 * Wi + x0) * C) + c);
   const float a01 = ld<T>(in, ((b + (long)y0 * Wi + x1) * C) + c);

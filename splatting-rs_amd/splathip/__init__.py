@@ -85,6 +85,13 @@ SIGNATURES = {
     "splat_kernel_gemm": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int,
                                     C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
     "splat_kernel_attention": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "splat_kernel_conv2d": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                      C.c_void_p]),
+    "splat_kernel_conv_transpose2d": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                                C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "splat_kernel_resize_bilinear": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                               C.c_void_p, C.c_int, C.c_int]),
 }
 
 _lib = None
@@ -244,6 +251,20 @@ class Context:
 
     def kernel_attention(self, dtype: int, qkv: int, out: int, S: int, L: int, heads: int):
         self.check(self._lib.splat_kernel_attention(self.handle, dtype, C.c_void_p(qkv), C.c_void_p(out), S, L, heads))
+
+    def kernel_conv2d(self, dtype, inp, V, H, W, Cin, w, Cout, ldw, ks, stride, bias, relu_in, act, res, out):
+        self.check(self._lib.splat_kernel_conv2d(self.handle, dtype, C.c_void_p(inp), V, H, W, Cin, C.c_void_p(w), Cout,
+                                                 ldw, ks, stride, C.c_void_p(bias), relu_in, act, C.c_void_p(res),
+                                                 C.c_void_p(out)))
+
+    def kernel_conv_transpose2d(self, dtype, inp, V, R, Cc, Cin, w, Cout, ldw, s, bias, out):
+        self.check(self._lib.splat_kernel_conv_transpose2d(self.handle, dtype, C.c_void_p(inp), V, R, Cc, Cin,
+                                                           C.c_void_p(w), Cout, ldw, s, C.c_void_p(bias),
+                                                           C.c_void_p(out)))
+
+    def kernel_resize_bilinear(self, dtype, inp, V, Hi, Wi, Cc, out, Ho, Wo):
+        self.check(self._lib.splat_kernel_resize_bilinear(self.handle, dtype, C.c_void_p(inp), V, Hi, Wi, Cc,
+                                                          C.c_void_p(out), Ho, Wo))
 
 
 def reference_ma_spec() -> dict:

@@ -94,3 +94,95 @@ def test_attention_matches_torch(ctx, dtype, S, L, heads):
     err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
     report("attention.err", err=f"{err:.2e}")
     assert err < (2e-5 if dtype == "f32" else 2e-2), err
+
+
+CONV_CASES = [
+    # (V, H, W, Cin, Cout, ks, stride, relu_in, act, residual)
+    (1, 5, 7, 8, 8, 3, 1, 0, 0, False),
+    (2, 16, 12, 48, 64, 3, 1, 0, 0, False),
+    (2, 16, 12, 64, 64, 3, 1, 1, 1, True),
+    (1, 27, 36, 384, 384, 3, 2, 0, 0, False),
+    (3, 13, 9, 32, 7, 3, 1, 0, 1, False),
+    (2, 10, 11, 96, 256, 1, 1, 0, 0, True),
+    (1, 28, 37, 256, 128, 3, 1, 0, 0, False),
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("V,H,W,Cin,Cout,ks,stride,relu_in,act,residual", CONV_CASES)
+def test_conv2d_matches_torch(ctx, dtype, V, H, W, Cin, Cout, ks, stride, relu_in, act, residual):
+    report("conv2d", dtype=dtype, V=V, H=H, W=W, Cin=Cin, Cout=Cout, ks=ks, stride=stride)
+    code, tdt = _dt(dtype)
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(V * 31 + H * 7 + Cin + Cout)
+    x = torch.randn(V, Cin, H, W, generator=g).to(tdt)
+    w = (torch.randn(Cout, Cin, ks, ks, generator=g) * 0.05).to(tdt)
+    b = torch.randn(Cout, generator=g)
+    K = ks * ks * Cin
+    ldw = (K + 63) // 64 * 64
+    wp = torch.zeros(Cout, ldw, dtype=tdt)
+    wp[:, :K] = w.permute(0, 2, 3, 1).reshape(Cout, K)
+    pad = ks // 2
+    Ho, Wo = (H + 2 * pad - ks) // stride + 1, (W + 2 * pad - ks) // stride + 1
+    xin = torch.relu(x.double()) if relu_in else x.double()
+    ref = F.conv2d(xin, w.double(), b.double(), stride=stride, padding=pad)
+    if act == 1:
+        ref = torch.relu(ref)
+    res = None
+    if residual:
+        res = torch.randn(V, Cout, Ho, Wo, generator=g).to(tdt)
+        ref = ref + res.double()
+    dx = x.permute(0, 2, 3, 1).contiguous().cuda()
+    dres = res.permute(0, 2, 3, 1).contiguous().cuda() if residual else None
+    out = torch.empty(V, Ho, Wo, Cout, dtype=tdt, device="cuda")
+    dw, db = wp.cuda(), b.cuda()
+    ctx.kernel_conv2d(code, dx.data_ptr(), V, H, W, Cin, dw.data_ptr(), Cout, ldw, ks, stride, db.data_ptr(),
+                      relu_in, act, dres.data_ptr() if residual else 0, out.data_ptr())
+    ctx.synchronize()
+    got = out.cpu().double().permute(0, 3, 1, 2)
+    err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
+    report("conv2d.err", err=f"{err:.2e}")
+    assert err < (1e-5 if dtype == "f32" else 8e-3), err
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("V,R,Cc,Cin,Cout,s", [(1, 3, 4, 48, 48, 4), (2, 27, 36, 96, 96, 2), (2, 5, 3, 32, 16, 4)])
+def test_conv_transpose2d_matches_torch(ctx, dtype, V, R, Cc, Cin, Cout, s):
+    report("convT", dtype=dtype, V=V, R=R, C=Cc, Cin=Cin, Cout=Cout, s=s)
+    code, tdt = _dt(dtype)
+    g = torch.Generator().manual_seed(R * 100 + Cc + s)
+    x = torch.randn(V, Cin, R, Cc, generator=g).to(tdt)
+    w = (torch.randn(Cin, Cout, s, s, generator=g) * 0.05).to(tdt)
+    b = torch.randn(Cout, generator=g)
+    ref = torch.nn.functional.conv_transpose2d(x.double(), w.double(), b.double(), stride=s)
+    ldw = (Cin + 63) // 64 * 64
+    wp = torch.zeros(s * s * Cout, ldw, dtype=tdt)
+    wp[:, :Cin] = w.permute(2, 3, 1, 0).reshape(s * s * Cout, Cin)
+    bx = b.repeat(s * s)
+    dx = x.permute(0, 2, 3, 1).contiguous().cuda()
+    out = torch.empty(V, R * s, Cc * s, Cout, dtype=tdt, device="cuda")
+    dw, db = wp.cuda(), bx.cuda()
+    ctx.kernel_conv_transpose2d(code, dx.data_ptr(), V, R, Cc, Cin, dw.data_ptr(), Cout, ldw, s, db.data_ptr(),
+                                out.data_ptr())
+    ctx.synchronize()
+    got = out.cpu().double().permute(0, 3, 1, 2)
+    err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
+    assert err < (1e-5 if dtype == "f32" else 8e-3), err
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("V,Hi,Wi,C,Ho,Wo", [(1, 4, 3, 8, 8, 6), (2, 14, 18, 64, 27, 36), (1, 224, 296, 32, 392, 518),
+                                              (1, 1, 5, 4, 3, 10), (2, 7, 7, 16, 7, 7)])
+def test_resize_bilinear_matches_torch(ctx, dtype, V, Hi, Wi, C, Ho, Wo):
+    report("resize", dtype=dtype, V=V, Hi=Hi, Wi=Wi, C=C, Ho=Ho, Wo=Wo)
+    code, tdt = _dt(dtype)
+    g = torch.Generator().manual_seed(Hi * 100 + Wi + Ho)
+    x = torch.randn(V, C, Hi, Wi, generator=g).to(tdt)
+    ref = torch.nn.functional.interpolate(x.double(), size=(Ho, Wo), mode="bilinear", align_corners=True)
+    dx = x.permute(0, 2, 3, 1).contiguous().cuda()
+    out = torch.empty(V, Ho, Wo, C, dtype=tdt, device="cuda")
+    ctx.kernel_resize_bilinear(code, dx.data_ptr(), V, Hi, Wi, C, out.data_ptr(), Ho, Wo)
+    ctx.synchronize()
+    got = out.cpu().double().permute(0, 3, 1, 2)
+    err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
+    assert err < (1e-6 if dtype == "f32" else 8e-3), err
