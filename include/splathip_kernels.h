@@ -36,6 +36,19 @@ int splat_kernel_conv2d(splat_ctx* ctx, int dtype, const void* in, int V, int H,
 int splat_kernel_conv_transpose2d(splat_ctx* ctx, int dtype, const void* in, int V, int R, int C, int Cin,
                                   const void* w, int Cout, int ldw, int s, const float* bias, void* out);
 
+/* Per-kernel-class timing of the following forwards: HIP events around every launch on the
+ * context's stream, with each launch's algorithmic work. Graph replay is bypassed while on. */
+typedef struct splat_kernel_stat {
+  char name[32];
+  int launches;
+  double ms;     /* summed launch durations */
+  double flops;  /* summed algorithmic flops (2 * multiply-adds) */
+  double bytes;  /* summed algorithmic bytes (inputs read once + outputs written once) */
+} splat_kernel_stat;
+int splat_profile_begin(splat_ctx* ctx);
+/* Synchronises, stops recording and writes up to `max` classes (largest time first). */
+int splat_profile_end(splat_ctx* ctx, splat_kernel_stat* stats, int max, int* count);
+
 /* Bilinear resize with align_corners=True (torch upsample_bilinear2d) of NHWC maps. */
 int splat_kernel_resize_bilinear(splat_ctx* ctx, int dtype, const void* in, int V, int Hi, int Wi, int C, void* out,
                                  int Ho, int Wo);

@@ -244,6 +244,8 @@ void attention(const Exec& ex, const AttnArgs& a) {
   SPLAT_CHECK(a.ld % ke == 0 && a.ldo % 4 == 0 && a.ld >= (long)a.heads * 64, BAD_ARGUMENT, "attention: strides");
   SPLAT_CHECK(a.seqs == 1 || a.seq_stride >= a.L, BAD_ARGUMENT, "attention: overlapping sequences");
   if (ex.dry) return;
+  const double rows = double(a.seqs) * a.L * a.heads;
+  ProfScope ps(ex, "attention", 4.0 * rows * a.L * 64, 4.0 * rows * 64 * (a.dt == F32 ? 4 : 2));
   dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
   const float c = 0.125f * 1.4426950408889634f;
   if (a.dt == F32) hipLaunchKernelGGL(attn_kernel<float>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);

@@ -1,6 +1,8 @@
 // The C ABI (include/splathip.h): argument checks, error mapping and host<->device staging
 // around the models. Nothing throws across this boundary.
+#include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 
 #include "runtime.h"
@@ -48,7 +50,7 @@ void check_images(const float* images, int V, int H, int W) {
 
 void* staging(Context* ctx, int slot, size_t bytes) { return ctx->staging_buffer(slot, bytes); }
 
-bool use_graphs(Context* ctx) { return ctx->graphs && !ctx->hooks.tap && !ctx->hooks.progress; }
+bool use_graphs(Context* ctx) { return ctx->graphs && !ctx->hooks.tap && !ctx->hooks.progress && !ctx->ex.prof; }
 
 void da3_device(Context* ctx, const float* images, int V, int H, int W, const splat_da3_out& out, int32_t* ref) {
   SPLAT_CHECK(ctx->da3 != nullptr, NOT_LOADED, "no Depth Anything 3 model loaded");
@@ -325,6 +327,46 @@ int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out
     a.seqs = S;
     a.seq_stride = L;
     attention(C(ctx)->ex, a);
+  });
+}
+
+int splat_profile_begin(splat_ctx* ctx) {
+  return guard(C(ctx), [&] {
+    Context* c = C(ctx);
+    if (!c->profiler) c->profiler = std::make_unique<Profiler>();
+    c->ex.prof = c->profiler.get();
+  });
+}
+
+int splat_profile_end(splat_ctx* ctx, splat_kernel_stat* stats, int max, int* count) {
+  return guard(C(ctx), [&] {
+    Context* c = C(ctx);
+    SPLAT_CHECK(c->profiler != nullptr, BAD_ARGUMENT, "profiling was not started");
+    SPLAT_HIP(hipStreamSynchronize(c->stream));
+    std::map<std::string, splat_kernel_stat> agg;
+    for (auto& r : c->profiler->recs) {
+      float ms = 0.f;
+      SPLAT_HIP(hipEventElapsedTime(&ms, r.e0, r.e1));
+      auto& s = agg[r.name];
+      s.launches += 1;
+      s.ms += ms;
+      s.flops += r.flops;
+      s.bytes += r.bytes;
+      (void)hipEventDestroy(r.e0);
+      (void)hipEventDestroy(r.e1);
+    }
+    c->profiler->recs.clear();
+    c->ex.prof = nullptr;
+    std::vector<std::pair<std::string, splat_kernel_stat>> v(agg.begin(), agg.end());
+    std::sort(v.begin(), v.end(), [](auto& a, auto& b) { return a.second.ms > b.second.ms; });
+    int n = 0;
+    for (auto& kv : v) {
+      if (n >= max || !stats) break;
+      splat_kernel_stat s = kv.second;
+      std::snprintf(s.name, sizeof(s.name), "%s", kv.first.c_str());
+      stats[n++] = s;
+    }
+    if (count) *count = n;
   });
 }
 

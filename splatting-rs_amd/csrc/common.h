@@ -6,6 +6,7 @@
 #include <cstddef>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace splat {
 
@@ -63,11 +64,44 @@ template <> __host__ __device__ inline bf16 from_f<bf16>(float v) { return f2bf(
 
 // --- execution context for launches -------------------------------------------------------
 
+// Per-launch timing records: HIP events around each launch on the launch's own stream, with
+// the launch's algorithmic work (2*MAC flops, bytes of inputs read once + outputs written once).
+struct ProfRecord {
+  const char* name;
+  double flops, bytes;
+  hipEvent_t e0, e1;
+};
+struct Profiler {
+  std::vector<ProfRecord> recs;
+};
+
 // Every launcher receives an Exec. With `dry` set, launchers only validate their arguments
 // and return: the forward runs once that way to size the activation arena.
 struct Exec {
   hipStream_t stream = nullptr;
   bool dry = false;
+  Profiler* prof = nullptr;
+};
+
+// Records one launch when profiling: construct right before the launch, destroyed after it.
+struct ProfScope {
+  const Exec& ex;
+  ProfRecord rec{};
+  bool on;
+  ProfScope(const Exec& e, const char* name, double flops, double bytes) : ex(e), on(e.prof != nullptr && !e.dry) {
+    if (!on) return;
+    rec.name = name;
+    rec.flops = flops;
+    rec.bytes = bytes;
+    (void)hipEventCreate(&rec.e0);
+    (void)hipEventCreate(&rec.e1);
+    (void)hipEventRecord(rec.e0, ex.stream);
+  }
+  ~ProfScope() {
+    if (!on) return;
+    (void)hipEventRecord(rec.e1, ex.stream);
+    ex.prof->recs.push_back(rec);
+  }
 };
 
 inline int cdiv(long a, long b) { return int((a + b - 1) / b); }

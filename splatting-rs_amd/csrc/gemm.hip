@@ -256,6 +256,11 @@ void gemm(const Exec& ex, const GemmArgs& a) {
     SPLAT_CHECK((long)a.ct_s * a.ct_s * a.ct_Cout == a.N && (long)a.V * a.ct_R * a.ct_C == a.M, BAD_ARGUMENT,
                 "gemm: convT geometry");
   if (ex.dry || a.M == 0) return;
+  const double es = a.dt == F32 ? 4 : 2, mn = double(a.M) * a.N;
+  const double abytes = a.amode == A_ROWS ? double(a.M) * a.K * es : double(a.V) * a.Hi * a.Wi * a.Cin * es;
+  const double bytes = abytes + double(a.N) * a.K * es + mn * (a.out_f32 ? 4 : es) +
+                       (a.res ? mn * (a.res_f32 ? 4 : es) : 0) + (a.res2 ? mn * (a.res2_f32 ? 4 : es) : 0);
+  ProfScope ps(ex, a.amode == A_ROWS ? "gemm" : "conv_igemm", 2.0 * mn * a.K, bytes);
   if (a.dt == F32) launch_typed<float>(ex, a);
   else launch_typed<bf16>(ex, a);
 }

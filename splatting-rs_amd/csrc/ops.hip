@@ -56,6 +56,7 @@ void layer_norm(const Exec& ex, int in_dt, const void* in, long ldin, int out_dt
   SPLAT_CHECK(in_dt_ok(in_dt) && in_dt_ok(out_dt) && rows >= 0 && n > 0, BAD_ARGUMENT, "layer_norm args");
   SPLAT_CHECK((w == nullptr) == (b == nullptr), BAD_ARGUMENT, "layer_norm: weight and bias come together");
   if (ex.dry || rows == 0) return;
+  ProfScope ps(ex, "layer_norm", 0, double(rows) * n * (dtype_size(in_dt) + dtype_size(out_dt)));
   dim3 grid(cdiv(rows, 4));
 #define LNL(TI, TO) hipLaunchKernelGGL((ln_kernel<TI, TO>), grid, dim3(256), 0, ex.stream, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off)
   if (in_dt == F32 && out_dt == F32) LNL(float, float);
@@ -131,6 +132,7 @@ void qk_norm_rope(const Exec& ex, int dt, void* qkv, int rows, int dim, const fl
   SPLAT_CHECK(!rope || cs != nullptr, BAD_ARGUMENT, "qk_norm_rope: missing rope table");
   if (rope && !across) SPLAT_CHECK((n - 1) / cols + 1 < npos && cols + 1 <= npos, BAD_ARGUMENT, "rope table too small");
   if (ex.dry || rows == 0) return;
+  ProfScope ps(ex, "qk_norm_rope", 0, 4.0 * rows * dim * dtype_size(dt));
   const long threads = (long)rows * (dim / 64) * 2;
   dim3 grid(cdiv(threads, 256));
   if (dt == F32) hipLaunchKernelGGL(qk_kernel<float>, grid, dim3(256), 0, ex.stream, qkv, rows, dim, qw, qb, kw, kb, n, cols, across, cs, npos, rope);
@@ -161,6 +163,7 @@ void im2col_patch(const Exec& ex, int dt, const float* img, int V, int H, int W,
   SPLAT_CHECK(H % 14 == 0 && W % 14 == 0 && kpad >= 588, BAD_ARGUMENT, "im2col args");
   if (ex.dry) return;
   const long total = (long)V * (H / 14) * (W / 14) * kpad;
+  ProfScope ps(ex, "im2col_patch", 0, double(V) * 3 * H * W * 4 + double(total) * dtype_size(dt));
   dim3 grid(cdiv(total, 256));
   if (dt == F32) hipLaunchKernelGGL(im2col_kernel<float>, grid, dim3(256), 0, ex.stream, img, V, H, W, out, kpad);
   else hipLaunchKernelGGL(im2col_kernel<bf16>, grid, dim3(256), 0, ex.stream, img, V, H, W, out, kpad);
@@ -217,6 +220,7 @@ void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int 
   SPLAT_CHECK(Ho <= Hf && Wo <= Wf && Hi > 0 && Wi > 0, BAD_ARGUMENT, "resize args");
   if (ex.dry) return;
   const long total = (long)V * Ho * Wo * C;
+  ProfScope ps(ex, "resize_bilinear", 0, (double(V) * Hi * Wi * C + double(total)) * dtype_size(dt) + (addtab ? double(Ho) * Wo * C * 4 : 0));
   dim3 grid(cdiv(total, 256));
   if (dt == F32) hipLaunchKernelGGL(resize_kernel<float>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
   else hipLaunchKernelGGL(resize_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
@@ -286,6 +290,8 @@ void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, 
   SPLAT_CHECK(mode != PW_DEPTH || cout == 2, BAD_ARGUMENT, "depth head has 2 channels");
   SPLAT_CHECK(mode != PW_MA || cout == 6, BAD_ARGUMENT, "MapAnything head has 6 channels");
   if (ex.dry || pix == 0) return;
+  const double obytes = mode == PW_MA ? (o0 ? 24.0 : 0) + (o1 ? 12.0 : 0) + (o2 ? 4.0 : 0) + (o3 ? 1.0 : 0) : 4.0 * cout;
+  ProfScope ps(ex, "pointwise_head", 2.0 * pix * cin * cout, double(pix) * (cin * dtype_size(dt) + obytes));
   dim3 grid(cdiv(pix, 256));
   if (dt == F32) hipLaunchKernelGGL(pw_kernel<float>, grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale);
   else hipLaunchKernelGGL(pw_kernel<bf16>, grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale);
@@ -316,6 +322,7 @@ void small_linear(const Exec& ex, int wdt, const float* x, long ldx, int M, int 
                   const float* b, float* y, long ldy, int N, int act) {
   SPLAT_CHECK(ldw >= K && ldx >= K && ldy >= N, BAD_ARGUMENT, "small_linear strides");
   if (ex.dry || M == 0) return;
+  ProfScope ps(ex, "small_linear", 2.0 * M * N * K, double(N) * K * dtype_size(wdt) + 4.0 * M * (K + N));
   dim3 grid(cdiv(N, 4));
   if (wdt == F32) hipLaunchKernelGGL(small_linear_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
   else hipLaunchKernelGGL(small_linear_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
@@ -452,6 +459,7 @@ __global__ void da3_hook_kernel(const float* within, const float* xs, int V, int
 void da3_hook(const Exec& ex, int dt, const float* within, const float* xs, int V, int n, int dim, const float* bnw,
               const float* bnb, const float* hnw, const float* hnb, void* out, float* cam_out) {
   if (ex.dry) return;
+  ProfScope ps(ex, "da3_hook", 0, double(V) * n * dim * 8 + double(V) * (n - 1) * 2 * dim * dtype_size(dt));
   dim3 grid(cdiv((long)V * n, 4));
   if (dt == F32) hipLaunchKernelGGL(da3_hook_kernel<float>, grid, dim3(256), 0, ex.stream, within, xs, V, n, dim, bnw, bnb, hnw, hnb, out, cam_out);
   else hipLaunchKernelGGL(da3_hook_kernel<bf16>, grid, dim3(256), 0, ex.stream, within, xs, V, n, dim, bnw, bnb, hnw, hnb, out, cam_out);
@@ -510,6 +518,7 @@ __global__ void swiglu_kernel(const void* x12, int rows, int hidden, void* out) 
 
 void swiglu_gate(const Exec& ex, int dt, const void* x12, int rows, int hidden, void* out) {
   if (ex.dry || rows == 0) return;
+  ProfScope ps(ex, "swiglu_gate", 0, 3.0 * rows * hidden * dtype_size(dt));
   dim3 grid(cdiv((long)rows * hidden, 256));
   if (dt == F32) hipLaunchKernelGGL(swiglu_kernel<float>, grid, dim3(256), 0, ex.stream, x12, rows, hidden, out);
   else hipLaunchKernelGGL(swiglu_kernel<bf16>, grid, dim3(256), 0, ex.stream, x12, rows, hidden, out);
@@ -528,6 +537,7 @@ __global__ void mean_rows_kernel(const void* in, int groups, int P, int C, float
 
 void mean_rows(const Exec& ex, int dt, const void* in, int groups, int P, int C, float* out) {
   if (ex.dry) return;
+  ProfScope ps(ex, "mean_rows", 0, double(groups) * P * C * dtype_size(dt) + 4.0 * groups * C);
   dim3 grid(cdiv((long)groups * C, 256));
   if (dt == F32) hipLaunchKernelGGL(mean_rows_kernel<float>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
   else hipLaunchKernelGGL(mean_rows_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);

@@ -257,6 +257,7 @@ class Context {
   std::string last_error;
   bool graphs = false;
   Hooks hooks;
+  std::unique_ptr<Profiler> profiler;
 
   std::unique_ptr<Da3Model> da3;
   std::unique_ptr<MaModel> ma;

@@ -57,6 +57,11 @@ class MaOutC(C.Structure):
                 ("points", C.c_void_p), ("conf", C.c_void_p), ("mask", C.c_void_p)]
 
 
+class KernelStatC(C.Structure):
+    _fields_ = [("name", C.c_char * 32), ("launches", C.c_int), ("ms", C.c_double), ("flops", C.c_double),
+                ("bytes", C.c_double)]
+
+
 PROGRESS_FN = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_void_p)
 TAP_FN = C.CFUNCTYPE(None, C.c_int, C.POINTER(C.c_float), C.c_int, C.c_int, C.c_void_p)
 
@@ -85,6 +90,8 @@ SIGNATURES = {
     "splat_kernel_gemm": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int,
                                     C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
     "splat_kernel_attention": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "splat_profile_begin": (C.c_int, [C.c_void_p]),
+    "splat_profile_end": (C.c_int, [C.c_void_p, C.POINTER(KernelStatC), C.c_int, C.POINTER(C.c_int)]),
     "splat_kernel_conv2d": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                       C.c_void_p]),
@@ -242,6 +249,18 @@ class Context:
 
     def ma_encode_device(self, images_ptr: int, V: int, H: int, W: int, tokens_ptr: int):
         self.check(self._lib.splat_ma_encode_device(self.handle, C.c_void_p(images_ptr), V, H, W, C.c_void_p(tokens_ptr)))
+
+    # --- profiling ----------------------------------------------------------------------------
+    def profile_begin(self):
+        self.check(self._lib.splat_profile_begin(self.handle))
+
+    def profile_end(self) -> list:
+        """[{name, launches, ms, flops, bytes}], largest total time first."""
+        stats = (KernelStatC * 64)()
+        n = C.c_int()
+        self.check(self._lib.splat_profile_end(self.handle, stats, 64, C.byref(n)))
+        return [{"name": s.name.decode(), "launches": s.launches, "ms": s.ms, "flops": s.flops, "bytes": s.bytes}
+                for s in stats[:n.value]]
 
     # --- kernels ------------------------------------------------------------------------------
     def kernel_gemm(self, dtype: int, A: int, M: int, K: int, W: int, N: int, ldw: int, bias: int, act: int,

@@ -172,20 +172,27 @@ def ma_shapes(spec: MaSpec) -> Shapes:
     return out
 
 
-def generate(shapes: Shapes, seed: int, layer_scale: float = 1e-5, std: float = 0.02) -> Dict[str, np.ndarray]:
-    tensors = {}
-    for name, (shape, kind) in shapes.items():
-        n = int(np.prod(shape))
-        if kind == LAYER_SCALE:
-            arr = np.full(n, layer_scale, dtype=np.float32)
-        else:
-            rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
-            arr = rng.standard_normal(n, dtype=np.float32)
-            arr *= np.float32(std)
-            if kind == LN_WEIGHT:
-                arr += np.float32(1.0)
-        tensors[name] = arr.reshape(shape)
-    return tensors
+def _one(name: str, shape, kind: int, seed: int, layer_scale: float, std: float) -> np.ndarray:
+    n = int(np.prod(shape))
+    if kind == LAYER_SCALE:
+        arr = np.full(n, layer_scale, dtype=np.float32)
+    else:
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+        arr = rng.standard_normal(n, dtype=np.float32)
+        arr *= np.float32(std)
+        if kind == LN_WEIGHT:
+            arr += np.float32(1.0)
+    return arr.reshape(shape)
+
+
+def generate(shapes: Shapes, seed: int, layer_scale: float = 1e-5, std: float = 0.02,
+             threads: int = 8) -> Dict[str, np.ndarray]:
+    """Every tensor of `shapes`, in a thread pool (the values do not depend on the pool)."""
+    from concurrent.futures import ThreadPoolExecutor
+    names = list(shapes)
+    with ThreadPoolExecutor(max_workers=max(1, threads)) as pool:
+        arrays = list(pool.map(lambda k: _one(k, shapes[k][0], shapes[k][1], seed, layer_scale, std), names))
+    return dict(zip(names, arrays))
 
 
 def save(path: str, tensors: Dict[str, np.ndarray]) -> None:
