@@ -59,6 +59,133 @@ __device__ inline float load_res(const void* p, long i, int f32) {
   return bf2f(reinterpret_cast<const bf16*>(p)[i]);
 }
 
+// Output index of element (m, n): row-major with optional row remap, or the transposed-conv
+// scatter (n = (dy*s + dx)*Cout + co of input pixel m -> NHWC output pixel).
+__device__ inline long out_index(const GemmArgs& p, long m, long n, long row) {
+  if (p.store != STORE_CONVT) return row * p.ldc + n;
+  const long t = n / p.ct_Cout, co = n - t * p.ct_Cout;
+  const long dy = t / p.ct_s, dx = t - dy * p.ct_s;
+  const long hw = (long)p.ct_R * p.ct_C;
+  const long vv = m / hw, rem = m - vv * hw;
+  const long rr = rem / p.ct_C, cc = rem - rr * p.ct_C;
+  return ((vv * p.ct_R * p.ct_s + rr * p.ct_s + dy) * ((long)p.ct_C * p.ct_s) + cc * p.ct_s + dx) * p.ct_Cout + co;
+}
+
+__device__ inline void load8(const void* p, long i, bool f32, float* v) {
+  if (f32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(p) + i);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = bf2f(bf16(w[k] & 0xffffu));
+      v[2 * k + 1] = bf2f(bf16(w[k] >> 16));
+    }
+  }
+}
+
+// Epilogue of 8 consecutive columns n..n+7 of row m: bias, activation, table add, LayerScale,
+// residuals, store. `vec`: all of them exist and every operand is 16-byte aligned for them.
+template <typename T>
+__device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool vec) {
+  const long row = p.rm_P ? (m / p.rm_P) * p.rm_n + p.rm_off + m % p.rm_P : m;
+  const bool rf = p.res_f32 || sizeof(T) == 4, rf2 = p.res2_f32 || sizeof(T) == 4;
+  if (vec) {
+    float t[8];
+    if (p.bias) { load8(p.bias, n, true, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    if (p.act == ACT_RELU) for (int k = 0; k < 8; ++k) v[k] = fmaxf(v[k], 0.f);
+    else if (p.act == ACT_GELU) for (int k = 0; k < 8; ++k) v[k] = gelu_erf(v[k]);
+    if (p.addtab) { load8(p.addtab, (m % p.addtab_period) * p.N + n, true, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    if (p.gamma) { load8(p.gamma, n, true, t); for (int k = 0; k < 8; ++k) v[k] *= t[k]; }
+    if (p.res) { load8(p.res, row * p.ldres + n, rf, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    if (p.res2) { load8(p.res2, row * p.ldres2 + n, rf2, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    const long idx = out_index(p, m, n, row);
+    if (p.out_f32) {
+      float* o = reinterpret_cast<float*>(p.out) + idx;
+      *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else if (sizeof(T) == 4) {
+      float* o = reinterpret_cast<float*>(p.out) + idx;
+      *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+      uint4 u;
+      u.x = uint32_t(f2bf(v[0])) | (uint32_t(f2bf(v[1])) << 16);
+      u.y = uint32_t(f2bf(v[2])) | (uint32_t(f2bf(v[3])) << 16);
+      u.z = uint32_t(f2bf(v[4])) | (uint32_t(f2bf(v[5])) << 16);
+      u.w = uint32_t(f2bf(v[6])) | (uint32_t(f2bf(v[7])) << 16);
+      *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p.out) + idx) = u;
+    }
+    return;
+  }
+  for (int k = 0; k < 8; ++k) {
+    const long nn = n + k;
+    if (nn >= p.N) break;
+    float x = v[k] + (p.bias ? p.bias[nn] : 0.f);
+    if (p.act == ACT_RELU) x = fmaxf(x, 0.f);
+    else if (p.act == ACT_GELU) x = gelu_erf(x);
+    if (p.addtab) x += p.addtab[(m % p.addtab_period) * p.N + nn];
+    if (p.gamma) x *= p.gamma[nn];
+    if (p.res) x += load_res<T>(p.res, row * p.ldres + nn, p.res_f32);
+    if (p.res2) x += load_res<T>(p.res2, row * p.ldres2 + nn, p.res2_f32);
+    const long idx = out_index(p, m, nn, row);
+    if (p.out_f32) reinterpret_cast<float*>(p.out)[idx] = x;
+    else reinterpret_cast<T*>(p.out)[idx] = from_f<T>(x);
+  }
+}
+
+// Epilogue through LDS: each wave stages one 32-row slab of its accumulators at a time
+// (from the 32x32 accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4,
+// column l%32 of each 32x32 tile), then every lane finishes runs of 8 consecutive columns.
+// `slab` is this wave's LDS region of 32 x (TN*32 + 4) floats; the block must be past its
+// last read of the main-loop LDS.
+template <typename T, int TM, int TN>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long wrow0, long wcol0, float* slab,
+                                         int lane, bool vec) {
+  constexpr int COLS = TN * 32, LD = COLS + 4, RUNS = COLS / 8;
+  const int g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) slab[(8 * (r >> 2) + 4 * g + (r & 3)) * LD + j * 32 + l32] = acc[i][j][r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int q = lane; q < 32 * RUNS; q += 64) {
+      const int rr = q / RUNS, cc = (q - rr * RUNS) * 8;
+      const long m = wrow0 + i * 32 + rr, n = wcol0 + cc;
+      if (m < p.M && n < p.N) {
+        float v[8];
+        const float4 a = *reinterpret_cast<const float4*>(slab + rr * LD + cc);
+        const float4 b = *reinterpret_cast<const float4*>(slab + rr * LD + cc + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        epi8<T>(p, v, m, n, vec && n + 8 <= p.N);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+// Whether the 8-column vector path is valid for every run of a launch (host side).
+inline bool epi_vec_ok(const GemmArgs& a, size_t es) {
+  auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const size_t oes = a.out_f32 ? 4 : es;
+  bool ok = a.N % 8 == 0 && al(a.out) && (a.bias == nullptr || al(a.bias)) && (a.gamma == nullptr || al(a.gamma)) &&
+            (a.addtab == nullptr || al(a.addtab));
+  if (a.store == STORE_CONVT) ok = ok && a.ct_Cout % 8 == 0;
+  else ok = ok && (a.ldc * oes) % 16 == 0;
+  if (a.res) ok = ok && al(a.res) && (a.ldres * (a.res_f32 ? 4 : es)) % 16 == 0;
+  if (a.res2) ok = ok && al(a.res2) && (a.ldres2 * (a.res2_f32 ? 4 : es)) % 16 == 0;
+  return ok;
+}
+
 constexpr int LDS_ROW = 144;  // bytes per tile row: 128 bytes of K + 16 bytes against bank conflicts
 
 template <typename T, int BM, int BN, int WM, int WN, int AMODE>
@@ -176,49 +303,212 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs p) {
     __syncthreads();
   }
 
-  // ---- epilogue
+  float* slab = reinterpret_cast<float*>(smem) + wave * 32 * (TN * 32 + 4);
+  epilogue<T, TM, TN>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec);
+}
+
+// ---------------------------------------------------------------------------------------
+// bf16 main path. Operand tiles stream from global memory straight into LDS through a
+// STAGES-deep ring (buffer_load_dwordx4 ... lds: 16 bytes per lane, one wave instruction fills
+// 1 KB = 8 tile rows of 128 bytes), so no registers stage them, and rows or K-chunks outside
+// the operands read as zero through the buffer descriptor's range check (offset 0x80000000).
+// Chunk c (16 bytes) of tile row r sits in slot c ^ ((r >> 1) & 7): the 16-lane phases of the
+// fragment reads (16 consecutive rows, one chunk) then touch 16 distinct 4-bank groups. The
+// loads are inline asm so that the compiler adds no waits of its own; the pipeline waits with
+// explicit vmcnt counts and one barrier per k-tile.
+
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ inline int32x4_t make_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  int32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane(int(uint32_t(a)));
+  r[1] = __builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32)));  // stride 0
+  r[2] = __builtin_amdgcn_readfirstlane(int(bytes));
+  r[3] = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+  return r;
+}
+
+typedef const __attribute__((address_space(3))) char* lds_cptr;
+
+__device__ inline uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((lds_cptr)p));  // generic -> LDS address space cast
+}
+
+__device__ inline void load_to_lds(const int32x4_t& rsrc, uint32_t voffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(__builtin_amdgcn_readfirstlane(int(lds))),
+               "v"(voffset), "s"(rsrc)
+               : "memory");
+}
+
+template <int N> __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+constexpr uint32_t OOB = 0x80000000u;
+
+template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, bool RELU>
+__global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  constexpr int AL = BM / 32, BL = BN / 32;  // load instructions per wave per k-tile
+  constexpr int LPT = AL + BL;
+  constexpr int STAGE = (BM + BN) * 128;
+  static_assert((STAGES - 2) * LPT <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int g = lane >> 5, l32 = lane & 31;
+
+  // Tile order: blocks b, b+8, ... land on one XCD; give each XCD a contiguous run of tiles,
+  // walked in groups of 8 tile rows so that neighbours share A and W panels in its L2.
+  const int nblk = tiles_m * tiles_n;
+  int bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int per_group = 8 * tiles_n;
+  const int first_m = (bid / per_group) * 8;
+  const int gsize = min(tiles_m - first_m, 8);
+  const int tm = first_m + (bid % per_group) % gsize;
+  const int tn = (bid % per_group) / gsize;
+  const long m0 = long(tm) * BM, n0 = long(tn) * BN;
+
+  // Each lane loads chunk c of tile row r = (i*4 + wave)*8 + lane/8 for instruction i; with
+  // slot lane%8 that chunk is slot ^ ((r >> 1) & 7), the same for every i.
+  const int lrow = lane >> 3;
+  const int c = (lane & 7) ^ ((4 * (wave & 1) + (lrow >> 1)) & 7);
+  const int32x4_t rw = make_rsrc(p.W, uint32_t(long(p.N) * p.ldw * 2));
+  uint32_t boff[BL];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const long n = n0 + wn * (BN / WN) + j * 32 + l32;
-    if (n >= p.N) continue;
-    const float bias = p.bias ? p.bias[n] : 0.f;
-    const float gam = p.gamma ? p.gamma[n] : 1.f;
-    long ct_t = 0, ct_co = 0, ct_dy = 0, ct_dx = 0;
-    if (p.store == STORE_CONVT) {
-      ct_t = n / p.ct_Cout;
-      ct_co = n - ct_t * p.ct_Cout;
-      ct_dy = ct_t / p.ct_s;
-      ct_dx = ct_t - ct_dy * p.ct_s;
+  for (int i = 0; i < BL; ++i) {
+    const long n = n0 + (i * 4 + wave) * 8 + lrow;
+    boff[i] = n < p.N ? uint32_t(n * p.ldw * 2 + c * 16) : OOB;
+  }
+  int32x4_t ra;
+  uint32_t aoff[AL];
+  int aiy[AL], aix[AL];
+  if (AMODE == A_ROWS) {
+    ra = make_rsrc(p.A, uint32_t(long(p.M) * p.lda * 2));
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+      const long m = m0 + (i * 4 + wave) * 8 + lrow;
+      aoff[i] = m < p.M ? uint32_t(m * p.lda * 2 + c * 16) : OOB;
     }
+  } else {
+    ra = make_rsrc(p.A, uint32_t(long(p.V) * p.Hi * p.Wi * p.Cin * 2));
+    const int hw = p.Ho * p.Wo;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const long m = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (m >= p.M) continue;
-        float v = acc[i][j][r] + bias;
-        if (p.act == ACT_RELU) v = fmaxf(v, 0.f);
-        else if (p.act == ACT_GELU) v = gelu_erf(v);
-        if (p.addtab) v += p.addtab[(m % p.addtab_period) * p.N + n];
-        v *= gam;
-        long row = p.rm_P ? (m / p.rm_P) * p.rm_n + p.rm_off + m % p.rm_P : m;
-        if (p.res) v += load_res<T>(p.res, row * p.ldres + n, p.res_f32);
-        if (p.res2) v += load_res<T>(p.res2, row * p.ldres2 + n, p.res2_f32);
-        long idx;
-        if (p.store == STORE_CONVT) {
-          const long hw = (long)p.ct_R * p.ct_C;
-          const long vv = m / hw, rem = m - vv * hw;
-          const long rr = rem / p.ct_C, cc = rem - rr * p.ct_C;
-          const long Wout = (long)p.ct_C * p.ct_s;
-          idx = ((vv * p.ct_R * p.ct_s + rr * p.ct_s + ct_dy) * Wout + cc * p.ct_s + ct_dx) * p.ct_Cout + ct_co;
-        } else {
-          idx = row * p.ldc + n;
-        }
-        if (p.out_f32) reinterpret_cast<float*>(p.out)[idx] = v;
-        else reinterpret_cast<T*>(p.out)[idx] = from_f<T>(v);
+    for (int i = 0; i < AL; ++i) {
+      const long m = m0 + (i * 4 + wave) * 8 + lrow;
+      if (m < p.M) {
+        const int v = int(m / hw), rem = int(m - long(v) * hw);
+        const int oy = rem / p.Wo, ox = rem - oy * p.Wo;
+        aiy[i] = oy * p.stride - p.pad;
+        aix[i] = ox * p.stride - p.pad;
+        aoff[i] = uint32_t(long(v) * p.Hi * p.Wi * p.Cin * 2);
+      } else {
+        aiy[i] = -(1 << 20);
+        aix[i] = 0;
+        aoff[i] = 0;
       }
     }
   }
+
+  auto issue = [&](int kt, int stage) {
+    const uint32_t sb = lds_addr(smem + stage * STAGE);
+    const int k = kt * 64 + c * 8;
+    if (AMODE == A_ROWS) {
+      const bool kin = k < p.K;
+#pragma unroll
+      for (int i = 0; i < AL; ++i)
+        load_to_lds(ra, (kin && aoff[i] != OOB) ? aoff[i] + kt * 128 : OOB, sb + (i * 4 + wave) * 1024);
+    } else {
+      const int tap = k / p.Cin, ci = k - tap * p.Cin;
+      const int ky = tap / p.ks, kx = tap - ky * p.ks;
+      const bool kin = k < p.K;
+#pragma unroll
+      for (int i = 0; i < AL; ++i) {
+        const int iy = aiy[i] + ky, ix = aix[i] + kx;
+        const bool ok = kin && iy >= 0 && iy < p.Hi && ix >= 0 && ix < p.Wi;
+        load_to_lds(ra, ok ? aoff[i] + uint32_t((iy * p.Wi + ix) * p.Cin + ci) * 2 : OOB, sb + (i * 4 + wave) * 1024);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BL; ++i)
+      load_to_lds(rw, boff[i] != OOB ? boff[i] + kt * 128 : OOB, sb + BM * 128 + (i * 4 + wave) * 1024);
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int sw = (l32 >> 1) & 7;
+  const int arow0 = (wm * (BM / WM) + l32) * 128, brow0 = (BM + wn * (BN / WN) + l32) * 128;
+  const int nk = (p.K + 63) / 64;
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nk) issue(s, s);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * LPT>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+    const char* sb = smem + (kt % STAGES) * STAGE;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int off = ((2 * s + g) ^ sw) * 16;
+      uint4 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const uint4*>(sb + arow0 + i * 32 * 128 + off);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const uint4*>(sb + brow0 + j * 32 * 128 + off);
+      if (RELU) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[i] = Mfma<bf16>::relu(fa[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) Mfma<bf16>::mma(acc[i][j], fa[i], fb[j]);
+    }
+  }
+  __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
+  float* slab = reinterpret_cast<float*>(smem) + wave * 32 * (TN * 32 + 4);
+  epilogue<bf16, TM, TN>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec);
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+static void launch_bf16(const Exec& ex, const GemmArgs& a) {
+  const int tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
+  dim3 grid(tm * tn);
+  if (a.amode == A_ROWS)
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, A_ROWS, false>), grid, dim3(256), 0, ex.stream, a, tm, tn);
+  else if (!a.relu_in)
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, A_CONV, false>), grid, dim3(256), 0, ex.stream, a, tm, tn);
+  else
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, A_CONV, true>), grid, dim3(256), 0, ex.stream, a, tm, tn);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// Tile choice: the fewest "rounds" of 256 CUs weighted by a per-tile cost relative to the
+// 256x256 tile (smaller tiles re-read more operand bytes through LDS per flop).
+static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
+  if (a.N <= 32) return launch_bf16<256, 32, 4, 1, 4>(ex, a);
+  if (a.N <= 64) return launch_bf16<256, 64, 4, 1, 3>(ex, a);
+  struct Cand { int bm, bn; double eff; };
+  const Cand cands[] = {{256, 256, 1.0}, {256, 128, 0.85}, {128, 128, 0.65}};
+  double best = 1e30;
+  int pick = 0;
+  for (int i = 0; i < 3; ++i) {
+    const long tiles = long(cdiv(a.M, cands[i].bm)) * cdiv(a.N, cands[i].bn);
+    const long rounds = (tiles + 255) / 256;
+    const double cost = double(rounds) * cands[i].bm * cands[i].bn / cands[i].eff;
+    if (cost < best * 0.999) { best = cost; pick = i; }
+  }
+  if (pick == 0) launch_bf16<256, 256, 2, 2, 2>(ex, a);
+  else if (pick == 1) launch_bf16<256, 128, 2, 2, 3>(ex, a);
+  else launch_bf16<128, 128, 2, 2, 4>(ex, a);
 }
 
 template <typename T, int BM, int BN, int WM, int WN>
@@ -233,6 +523,10 @@ static void launch_cfg(const Exec& ex, const GemmArgs& a) {
 
 template <typename T>
 static void launch_typed(const Exec& ex, const GemmArgs& a) {
+  if constexpr (sizeof(T) == 2) {
+    const double abytes = a.amode == A_ROWS ? double(a.M) * a.lda * 2 : double(a.V) * a.Hi * a.Wi * a.Cin * 2;
+    if (abytes < 2147483648.0 && double(a.N) * a.ldw * 2 < 2147483648.0) return launch_bf16_auto(ex, a);
+  }
   const long tiles128 = (long)cdiv(a.M, 128) * cdiv(a.N, 128);
   if (a.N <= 32) launch_cfg<T, 256, 32, 4, 1>(ex, a);
   else if (a.N <= 64) launch_cfg<T, 256, 64, 4, 1>(ex, a);
@@ -240,7 +534,9 @@ static void launch_typed(const Exec& ex, const GemmArgs& a) {
   else launch_cfg<T, 64, 128, 1, 4>(ex, a);
 }
 
-void gemm(const Exec& ex, const GemmArgs& a) {
+void gemm(const Exec& ex, const GemmArgs& args) {
+  GemmArgs a = args;
+  a.epi_vec = epi_vec_ok(a, a.dt == F32 ? 4 : 2) ? 1 : 0;
   const int ke = a.dt == F32 ? 4 : 8;
   SPLAT_CHECK(a.M >= 0 && a.N > 0 && a.K > 0, BAD_ARGUMENT, "gemm: bad sizes");
   SPLAT_CHECK(a.K % ke == 0, BAD_ARGUMENT, "gemm: K must be a multiple of the 16-byte chunk");

@@ -42,6 +42,7 @@ struct GemmArgs {
   int rm_P = 0, rm_n = 0, rm_off = 0;
   int store = STORE_ROWS;
   int ct_s = 1, ct_R = 0, ct_C = 0, ct_Cout = 0;
+  int epi_vec = 0;  // set by gemm(): the epilogue may use 16-byte vector accesses
 };
 void gemm(const Exec& ex, const GemmArgs& a);
 
