@@ -32,7 +32,7 @@ template <> struct AttnOps<bf16> {
       uint32_t* pw = reinterpret_cast<uint32_t*>(&pf);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        pw[i] = uint32_t(f2bf(s[8 * hh + 2 * i])) | (uint32_t(f2bf(s[8 * hh + 2 * i + 1])) << 16);
+        pw[i] = pack_bf16x2(s[8 * hh + 2 * i], s[8 * hh + 2 * i + 1]);
       o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf), __builtin_bit_cast(bf16x8_t, pf),
                                                   o, 0, 0, 0);
     }
@@ -43,8 +43,8 @@ template <> struct AttnOps<bf16> {
   }
   __device__ static inline void store4(void* dst, const float* v) {
     uint2 w;
-    w.x = uint32_t(f2bf(v[0])) | (uint32_t(f2bf(v[1])) << 16);
-    w.y = uint32_t(f2bf(v[2])) | (uint32_t(f2bf(v[3])) << 16);
+    w.x = pack_bf16x2(v[0], v[1]);
+    w.y = pack_bf16x2(v[2], v[3]);
     *reinterpret_cast<uint2*>(dst) = w;
   }
 };
@@ -238,6 +238,249 @@ __global__ void __launch_bounds__(ATTN_WAVES * 64) attn_kernel(const AttnArgs p,
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// bf16 main path. Each wave owns QT*32 queries, so every K and V^T fragment read from LDS
+// feeds QT matrix-core ops. K tiles stream straight into LDS (buffer_load_dwordx4 ... lds,
+// rows of 128 bytes with chunk c of row r in slot c ^ ((r >> 1) & 7)); V goes through
+// registers to be stored transposed. Rows past the sequence read as zero (buffer range check)
+// and are masked to -inf only in the last tile. The softmax keeps a reference max per query
+// and rescales O and the running sum only when a tile's max exceeds it by more than 2^8 (in
+// exp2 units): O and the sum always share the reference, so the result is exact and P stays
+// below 256.
+
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(3))) char* lds_cptr_a;
+
+namespace {
+
+__device__ inline int32x4_t make_rsrc_a(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  int32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane(int(uint32_t(a)));
+  r[1] = __builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32)));
+  r[2] = __builtin_amdgcn_readfirstlane(int(bytes));
+  r[3] = 0x00020000;
+  return r;
+}
+
+__device__ inline void load_lds_a(const int32x4_t& rsrc, uint32_t voffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(__builtin_amdgcn_readfirstlane(int(lds))),
+               "v"(voffset), "s"(rsrc)
+               : "memory");
+}
+
+template <int N> __device__ inline void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+}  // namespace
+
+template <int WAVES, int QT>
+__global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p, float c) {
+  constexpr int NT = WAVES * 64;
+  constexpr int KBYTES = 64 * 128;            // K tile: 64 keys x 128 bytes, swizzled, unpadded
+  constexpr int VROW = 64 * 2 + 8;            // V^T row: 64 keys (bf16) + pad
+  constexpr int VBYTES = 64 * VROW;
+  constexpr int KL = 8 / WAVES;               // K load instructions per wave per tile
+  constexpr int VB = 256 / NT;                // 4x4 V blocks per thread per tile
+  static_assert(WAVES == 2 || WAVES == 4, "the K-load swizzle assumes an even number of waves");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * (KBYTES + VBYTES)];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int h = blockIdx.y;
+  const int L = p.L;
+  const long base = long(blockIdx.z) * p.seq_stride;
+  const bf16* Q = reinterpret_cast<const bf16*>(p.q) + h * 64;
+  const bf16* V = reinterpret_cast<const bf16*>(p.v) + h * 64;
+  const int q0 = (blockIdx.x * WAVES + wave) * (QT * 32);
+
+  uint4 qf[QT][4];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qrow = q0 + qt * 32 + l32;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      qf[qt][st] = qrow < L ? *reinterpret_cast<const uint4*>(Q + (base + qrow) * p.ld + st * 16 + g * 8)
+                            : make_uint4(0, 0, 0, 0);
+  }
+
+  // K rows: sequence row s -> byte offset within the buffer that starts at the sequence's row 0
+  const bf16* Kseq = reinterpret_cast<const bf16*>(p.k) + base * p.ld + h * 64;
+  const int32x4_t rk = make_rsrc_a(Kseq, uint32_t(long(L) * p.ld * 2));
+  const int lrow = lane >> 3;
+  const int kc = (lane & 7) ^ ((4 * (wave & 1) + (lrow >> 1)) & 7);
+  auto issue_k = [&](int t, int buf) {
+    const uint32_t sb = uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_a)(smem + buf * (KBYTES + VBYTES))));
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const int row = (i * WAVES + wave) * 8 + lrow;
+      const int key = t * 64 + row;
+      load_lds_a(rk, key < L ? uint32_t(key * p.ld * 2 + kc * 16) : 0x80000000u, sb + (i * WAVES + wave) * 1024);
+    }
+  };
+  uint2 rv[VB][4];
+  auto load_v = [&](int t) {
+#pragma unroll
+    for (int b = 0; b < VB; ++b) {
+      const int blk = tid + b * NT, kq = blk >> 4, dq = blk & 15;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = t * 64 + 4 * kq + j;
+        rv[b][j] = key < L ? *reinterpret_cast<const uint2*>(V + (base + key) * p.ld + 4 * dq) : make_uint2(0, 0);
+      }
+    }
+  };
+  auto store_v = [&](int buf) {
+    char* vt = smem + buf * (KBYTES + VBYTES) + KBYTES;
+#pragma unroll
+    for (int b = 0; b < VB; ++b) {
+      const int blk = tid + b * NT, kq = blk >> 4, dq = blk & 15;
+      const uint16_t* e[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[j] = reinterpret_cast<const uint16_t*>(&rv[b][j]);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        uint2 w;
+        w.x = uint32_t(e[0][x]) | (uint32_t(e[1][x]) << 16);
+        w.y = uint32_t(e[2][x]) | (uint32_t(e[3][x]) << 16);
+        *reinterpret_cast<uint2*>(vt + (4 * dq + x) * VROW + 8 * kq) = w;
+      }
+    }
+  };
+
+  f32x16 o[QT][2];
+  float mref[QT], lsum[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    mref[qt] = -INFINITY;
+    lsum[qt] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { o[qt][0][r] = 0.f; o[qt][1][r] = 0.f; }
+  }
+  const int sw = (l32 >> 1) & 7;
+
+  auto tile = [&](int t, int buf, auto masked) {
+    const char* kb = smem + buf * (KBYTES + VBYTES);
+    const char* vt = kb + KBYTES;
+    f32x16 s[QT][2];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { s[qt][0][r] = 0.f; s[qt][1][r] = 0.f; }
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(kb + (kt2 * 32 + l32) * 128 + ((2 * st + g) ^ sw) * 16);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) AttnOps<bf16>::qk(s[qt][kt2], kf, qf[qt][st]);
+      }
+    if (decltype(masked)::value) {
+      const int k0 = t * 64;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (k0 + kt2 * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= L) s[qt][kt2][r] = -INFINITY;
+    }
+    bool grow = false;
+    float mnew[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float mx = s[qt][0][0];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[qt][0][r], s[qt][1][r]));
+      mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+      mnew[qt] = mx > mref[qt] + 8.f ? mx : mref[qt];
+      grow |= mnew[qt] != mref[qt];
+    }
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const float alpha = __builtin_amdgcn_exp2f(mref[qt] - mnew[qt]);
+        lsum[qt] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { o[qt][0][r] *= alpha; o[qt][1][r] *= alpha; }
+        mref[qt] = mnew[qt];
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float ps = 0.f;
+#pragma unroll
+      for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[qt][kt2][r], c, -mref[qt]));
+          s[qt][kt2][r] = e;
+          ps += e;
+        }
+      lsum[qt] += ps;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const char* vrow = vt + (dt * 32 + l32) * VROW;
+#pragma unroll
+      for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const char* vb = vrow + (kt2 * 32 + 16 * hh + 4 * g) * 2;
+          const uint2 lo = *reinterpret_cast<const uint2*>(vb);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vb + 16);
+          const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            uint4 pf;
+            uint32_t* pw = reinterpret_cast<uint32_t*>(&pf);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              pw[i] = pack_bf16x2(s[qt][kt2][8 * hh + 2 * i], s[qt][kt2][8 * hh + 2 * i + 1]);
+            o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf),
+                                                                __builtin_bit_cast(bf16x8_t, pf), o[qt][dt], 0, 0, 0);
+          }
+        }
+    }
+  };
+
+  const int ntiles = (L + 63) / 64;
+  issue_k(0, 0);
+  load_v(0);
+  store_v(0);
+  wait_vm<0>();
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) {
+      issue_k(t + 1, buf ^ 1);
+      load_v(t + 1);
+    }
+    if (t + 1 < ntiles) tile(t, buf, std::integral_constant<bool, false>{});
+    else tile(t, buf, std::integral_constant<bool, true>{});
+    if (t + 1 < ntiles) store_v(buf ^ 1);
+    wait_vm<0>();
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const float inv = 1.f / (lsum[qt] + __shfl_xor(lsum[qt], 32));
+    const int qrow = q0 + qt * 32 + l32;
+    if (qrow < L) {
+      bf16* O = reinterpret_cast<bf16*>(p.o) + (base + qrow) * p.ldo + h * 64;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = o[qt][dt][4 * q4 + e] * inv;
+          AttnOps<bf16>::store4(O + dt * 32 + 8 * q4 + 4 * g, v);
+        }
+    }
+  }
+}
+
 void attention(const Exec& ex, const AttnArgs& a) {
   const int ke = a.dt == F32 ? 4 : 8;
   SPLAT_CHECK(a.L > 0 && a.heads > 0 && a.seqs > 0, BAD_ARGUMENT, "attention: bad sizes");
@@ -246,10 +489,18 @@ void attention(const Exec& ex, const AttnArgs& a) {
   if (ex.dry) return;
   const double rows = double(a.seqs) * a.L * a.heads;
   ProfScope ps(ex, "attention", 4.0 * rows * a.L * 64, 4.0 * rows * 64 * (a.dt == F32 ? 4 : 2));
-  dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
   const float c = 0.125f * 1.4426950408889634f;
-  if (a.dt == F32) hipLaunchKernelGGL(attn_kernel<float>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);
-  else hipLaunchKernelGGL(attn_kernel<bf16>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);
+  if (a.dt == F32) {
+    dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
+    hipLaunchKernelGGL(attn_kernel<float>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);
+  } else if (long(a.L) * a.ld * 2 < 2147483648L && a.ld % 8 == 0 && a.ldo % 4 == 0) {
+    // 4 waves x 32 queries: two sub-tiles of queries per wave (QT = 2) measured slower on
+    // gfx950 (register pressure pushes the accumulators through AGPR moves).
+    hipLaunchKernelGGL((attn_bf16_kernel<4, 1>), dim3(cdiv(a.L, 128), a.heads, a.seqs), dim3(256), 0, ex.stream, a, c);
+  } else {
+    dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
+    hipLaunchKernelGGL(attn_kernel<bf16>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);
+  }
   SPLAT_HIP(hipGetLastError());
 }
 

@@ -45,13 +45,28 @@ __host__ __device__ inline float bf2f(bf16 v) {
   return f;
 }
 
-// Round to nearest even (NaN kept quiet).
+// Round to nearest even (NaN kept quiet); on the device the v_cvt_pk_bf16_f32 instruction.
 __host__ __device__ inline bf16 f2bf(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(bf16, static_cast<__bf16>(f));
+#else
   uint32_t u;
   __builtin_memcpy(&u, &f, 4);
   if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return bf16((u >> 16) | 0x40);
   u += 0x7fffu + ((u >> 16) & 1u);
   return bf16(u >> 16);
+#endif
+}
+
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+// Two floats -> packed bf16 pair (low = a); on the device one v_cvt_pk_bf16_f32.
+__host__ __device__ inline uint32_t pack_bf16x2(float a, float b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  bf16x2_hw v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+#else
+  return uint32_t(f2bf(a)) | (uint32_t(f2bf(b)) << 16);
+#endif
 }
 
 template <typename T> __host__ __device__ inline float to_f(T v);

@@ -113,10 +113,10 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
       *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
     } else {
       uint4 u;
-      u.x = uint32_t(f2bf(v[0])) | (uint32_t(f2bf(v[1])) << 16);
-      u.y = uint32_t(f2bf(v[2])) | (uint32_t(f2bf(v[3])) << 16);
-      u.z = uint32_t(f2bf(v[4])) | (uint32_t(f2bf(v[5])) << 16);
-      u.w = uint32_t(f2bf(v[6])) | (uint32_t(f2bf(v[7])) << 16);
+      u.x = pack_bf16x2(v[0], v[1]);
+      u.y = pack_bf16x2(v[2], v[3]);
+      u.z = pack_bf16x2(v[4], v[5]);
+      u.w = pack_bf16x2(v[6], v[7]);
       *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p.out) + idx) = u;
     }
     return;
