@@ -51,19 +51,95 @@ __global__ void ln_kernel(const void* in, long ldin, void* out, long ldout, int 
   }
 }
 
+// 4 consecutive elements as floats / from floats (16-byte fp32 or 8-byte bf16 accesses).
+template <typename T> __device__ inline float4 ld4(const void* p, long i);
+template <> __device__ inline float4 ld4<float>(const void* p, long i) {
+  return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+}
+template <> __device__ inline float4 ld4<bf16>(const void* p, long i) {
+  const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16*>(p) + i);
+  return make_float4(bf2f(bf16(u.x & 0xffffu)), bf2f(bf16(u.x >> 16)), bf2f(bf16(u.y & 0xffffu)), bf2f(bf16(u.y >> 16)));
+}
+template <typename T> __device__ inline void st4(void* p, long i, float4 v);
+template <> __device__ inline void st4<float>(void* p, long i, float4 v) {
+  *reinterpret_cast<float4*>(reinterpret_cast<float*>(p) + i) = v;
+}
+template <> __device__ inline void st4<bf16>(void* p, long i, float4 v) {
+  *reinterpret_cast<uint2*>(reinterpret_cast<bf16*>(p) + i) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+}
+
+// Register-resident LayerNorm: one wave per row, 4-element vector accesses, the row held in
+// MAXC float4 per lane; mean, then centred variance, from registers.
+template <typename TI, typename TO, int MAXC>
+__global__ void ln_vec_kernel(const void* in, long ldin, void* out, long ldout, int rows, int n, const float* w,
+                              const float* b, float eps, int rmP, int rmn, int rmoff) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+  if (wave >= rows) return;
+  const long rin = rmP ? (long)(wave / rmP) * rmn + rmoff + wave % rmP : wave;
+  const long ib = rin * ldin, ob = (long)wave * ldout;
+  const int nc = n >> 2;
+  float4 x[MAXC];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    const int c = lane + 64 * k;
+    x[k] = c < nc ? ld4<TI>(in, ib + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (x[k].x + x[k].y) + (x[k].z + x[k].w);
+  }
+  const float mean = wave_sum(s) / n;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    if (lane + 64 * k < nc) {
+      const float a = x[k].x - mean, bb = x[k].y - mean, cc = x[k].z - mean, d = x[k].w - mean;
+      q += (a * a + bb * bb) + (cc * cc + d * d);
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) / n + eps);
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    const int c = lane + 64 * k;
+    if (c < nc) {
+      float4 y = make_float4((x[k].x - mean) * rstd, (x[k].y - mean) * rstd, (x[k].z - mean) * rstd, (x[k].w - mean) * rstd);
+      if (w) {
+        const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c), bv = *reinterpret_cast<const float4*>(b + 4 * c);
+        y = make_float4(y.x * wv.x + bv.x, y.y * wv.y + bv.y, y.z * wv.z + bv.z, y.w * wv.w + bv.w);
+      }
+      st4<TO>(out, ob + 4 * c, y);
+    }
+  }
+}
+
+template <typename TI, typename TO>
+static void ln_launch(const Exec& ex, const void* in, long ldin, void* out, long ldout, int rows, int n, const float* w,
+                      const float* b, float eps, int rm_P, int rm_n, int rm_off) {
+  dim3 grid(cdiv(rows, 4));
+  const int per_lane = cdiv(n / 4, 64);
+  const bool vec = n % 4 == 0 && ldin % 4 == 0 && ldout % 4 == 0 && per_lane <= 16 &&
+                   (reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  if (!vec) {
+    hipLaunchKernelGGL((ln_kernel<TI, TO>), grid, dim3(256), 0, ex.stream, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  } else if (per_lane <= 2) {
+    hipLaunchKernelGGL((ln_vec_kernel<TI, TO, 2>), grid, dim3(256), 0, ex.stream, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  } else if (per_lane <= 4) {
+    hipLaunchKernelGGL((ln_vec_kernel<TI, TO, 4>), grid, dim3(256), 0, ex.stream, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  } else if (per_lane <= 8) {
+    hipLaunchKernelGGL((ln_vec_kernel<TI, TO, 8>), grid, dim3(256), 0, ex.stream, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  } else {
+    hipLaunchKernelGGL((ln_vec_kernel<TI, TO, 16>), grid, dim3(256), 0, ex.stream, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  }
+}
+
 void layer_norm(const Exec& ex, int in_dt, const void* in, long ldin, int out_dt, void* out, long ldout, int rows,
                 int n, const float* w, const float* b, float eps, int rm_P, int rm_n, int rm_off) {
   SPLAT_CHECK(in_dt_ok(in_dt) && in_dt_ok(out_dt) && rows >= 0 && n > 0, BAD_ARGUMENT, "layer_norm args");
   SPLAT_CHECK((w == nullptr) == (b == nullptr), BAD_ARGUMENT, "layer_norm: weight and bias come together");
   if (ex.dry || rows == 0) return;
   ProfScope ps(ex, "layer_norm", 0, double(rows) * n * (dtype_size(in_dt) + dtype_size(out_dt)));
-  dim3 grid(cdiv(rows, 4));
-#define LNL(TI, TO) hipLaunchKernelGGL((ln_kernel<TI, TO>), grid, dim3(256), 0, ex.stream, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off)
-  if (in_dt == F32 && out_dt == F32) LNL(float, float);
-  else if (in_dt == F32 && out_dt == BF16) LNL(float, bf16);
-  else if (in_dt == BF16 && out_dt == F32) LNL(bf16, float);
-  else LNL(bf16, bf16);
-#undef LNL
+  if (in_dt == F32 && out_dt == F32) ln_launch<float, float>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  else if (in_dt == F32) ln_launch<float, bf16>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  else if (out_dt == F32) ln_launch<bf16, float>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  else ln_launch<bf16, bf16>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -85,7 +161,13 @@ __global__ void qk_kernel(void* qkv, int rows, int dim, const float* qw, const f
   const float* b = which ? kb : qb;
   float v[64];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) v[i] = to_f<T>(x[i]);
+  for (int i = 0; i < 16; ++i) {
+    const float4 f = ld4<T>(x, 4 * i);
+    v[4 * i] = f.x;
+    v[4 * i + 1] = f.y;
+    v[4 * i + 2] = f.z;
+    v[4 * i + 3] = f.w;
+  }
   if (w) {
     float s = 0.f;
 #pragma unroll
@@ -123,7 +205,7 @@ __global__ void qk_kernel(void* qkv, int rows, int dim, const float* qw, const f
     }
   }
 #pragma unroll
-  for (int i = 0; i < 64; ++i) x[i] = from_f<T>(v[i]);
+  for (int i = 0; i < 16; ++i) st4<T>(x, 4 * i, make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]));
 }
 
 void qk_norm_rope(const Exec& ex, int dt, void* qkv, int rows, int dim, const float* qw, const float* qb,
@@ -215,11 +297,62 @@ __global__ void resize_kernel(const void* in, int V, int Hi, int Wi, int C, void
   st<T>(out, id, val);
 }
 
+// Same, 8 channels per thread (C % 8 == 0): the four source pixels and the output are read
+// and written as 8-channel vectors.
+template <typename T>
+__global__ void resize8_kernel(const void* in, int V, int Hi, int Wi, int C, void* out, int Hf, int Wf, int Ho, int Wo,
+                               const float* addtab, int relu) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int C8 = C >> 3;
+  const long total = (long)V * Ho * Wo * C8;
+  if (id >= total) return;
+  const int c = int(id % C8) * 8;
+  long r = id / C8;
+  const int ox = int(r % Wo);
+  r /= Wo;
+  const int oy = int(r % Ho);
+  const long v = r / Ho;
+  const double fy = Hf > 1 ? double(Hi - 1) * oy / double(Hf - 1) : 0.0;
+  const double fx = Wf > 1 ? double(Wi - 1) * ox / double(Wf - 1) : 0.0;
+  const int y0 = min(int(fy), Hi - 1), x0 = min(int(fx), Wi - 1);
+  const int y1 = y0 + (y0 < Hi - 1 ? 1 : 0), x1 = x0 + (x0 < Wi - 1 ? 1 : 0);
+  const float ly = float(fy - y0), lx = float(fx - x0);
+  const long b = v * Hi * Wi;
+  const long i00 = (b + (long)y0 * Wi + x0) * C + c, i01 = (b + (long)y0 * Wi + x1) * C + c;
+  const long i10 = (b + (long)y1 * Wi + x0) * C + c, i11 = (b + (long)y1 * Wi + x1) * C + c;
+  const long o = id * 8;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float4 a = ld4<T>(in, i00 + 4 * h), bq = ld4<T>(in, i01 + 4 * h);
+    const float4 cq = ld4<T>(in, i10 + 4 * h), d = ld4<T>(in, i11 + 4 * h);
+    float4 y;
+    y.x = (1.f - ly) * ((1.f - lx) * a.x + lx * bq.x) + ly * ((1.f - lx) * cq.x + lx * d.x);
+    y.y = (1.f - ly) * ((1.f - lx) * a.y + lx * bq.y) + ly * ((1.f - lx) * cq.y + lx * d.y);
+    y.z = (1.f - ly) * ((1.f - lx) * a.z + lx * bq.z) + ly * ((1.f - lx) * cq.z + lx * d.z);
+    y.w = (1.f - ly) * ((1.f - lx) * a.w + lx * bq.w) + ly * ((1.f - lx) * cq.w + lx * d.w);
+    if (addtab) {
+      const float4 t = *reinterpret_cast<const float4*>(addtab + ((long)oy * Wo + ox) * C + c + 4 * h);
+      y.x += t.x; y.y += t.y; y.z += t.z; y.w += t.w;
+    }
+    if (relu) { y.x = fmaxf(y.x, 0.f); y.y = fmaxf(y.y, 0.f); y.z = fmaxf(y.z, 0.f); y.w = fmaxf(y.w, 0.f); }
+    st4<T>(out, o + 4 * h, y);
+  }
+}
+
 void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int Wi, int C, void* out, int Hf, int Wf,
                      int Ho, int Wo, const float* addtab, int relu) {
   SPLAT_CHECK(Ho <= Hf && Wo <= Wf && Hi > 0 && Wi > 0, BAD_ARGUMENT, "resize args");
   if (ex.dry) return;
   const long total = (long)V * Ho * Wo * C;
+  if (C % 8 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(addtab) & 15) == 0) {
+    ProfScope ps(ex, "resize_bilinear", 0, (double(V) * Hi * Wi * C + double(total)) * dtype_size(dt) + (addtab ? double(Ho) * Wo * C * 4 : 0));
+    dim3 grid(cdiv(total / 8, 256));
+    if (dt == F32) hipLaunchKernelGGL(resize8_kernel<float>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+    else hipLaunchKernelGGL(resize8_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+    SPLAT_HIP(hipGetLastError());
+    return;
+  }
   ProfScope ps(ex, "resize_bilinear", 0, (double(V) * Hi * Wi * C + double(total)) * dtype_size(dt) + (addtab ? double(Ho) * Wo * C * 4 : 0));
   dim3 grid(cdiv(total, 256));
   if (dt == F32) hipLaunchKernelGGL(resize_kernel<float>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
@@ -284,8 +417,96 @@ __global__ void pw_kernel(int mode, const void* in, long pix, int hw, int cin, i
   }
 }
 
+// Cooperative form: LPP lanes per pixel (cin = 8*LPP), each lane holding 8 channels read as
+// one vector; dot products and LayerNorm statistics are reduced across the lane group.
+template <typename T, int LPP>
+__global__ void pw_coop_kernel(int mode, const void* in, long pix, int hw, int cin, int cout, const float* w,
+                               const float* b, float* o0, float* o1, float* o2, uint8_t* o3, const float* scale) {
+  __shared__ float sw[8 * 256];
+  __shared__ float sb[8];
+  for (int i = threadIdx.x; i < cout * cin; i += blockDim.x) sw[i] = w[i];
+  if (threadIdx.x < cout) sb[threadIdx.x] = b[threadIdx.x];
+  __syncthreads();
+  const long gt = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long px = gt / LPP;
+  const int sub = int(gt % LPP);
+  if (px >= pix) return;  // whole lane groups leave together (LPP divides 64)
+  const int c0 = sub * 8;
+  float x[8];
+  {
+    const float4 a = ld4<T>(in, px * cin + c0), bb = ld4<T>(in, px * cin + c0 + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = bb.x; x[5] = bb.y; x[6] = bb.z; x[7] = bb.w;
+  }
+  auto group_sum = [](float v) {
+#pragma unroll
+    for (int o = LPP / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+  };
+  if (mode == PW_RAY) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += x[k];
+    const float mean = group_sum(s) / cin;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q += (x[k] - mean) * (x[k] - mean);
+    const float rstd = rsqrtf(group_sum(q) / cin + 1e-5f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = fmaxf((x[k] - mean) * rstd, 0.f);
+  }
+  float acc[8];
+#pragma unroll
+  for (int o = 0; o < 8; ++o) {
+    float s = 0.f;
+    if (o < cout) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s += sw[o * cin + c0 + k] * x[k];
+    }
+    acc[o] = group_sum(s) + (o < cout ? sb[o] : 0.f);
+  }
+  if (sub != 0) return;
+  const long v = px / hw, q = px % hw;
+  if (mode == PW_DEPTH) {
+    o0[px] = expf(acc[0]);
+    o1[px] = 1.f + expf(acc[1]);
+  } else if (mode == PW_RAY) {
+    for (int o = 0; o < cout; ++o) o0[(v * cout + o) * hw + q] = acc[o];
+  } else {
+    if (o0)
+      for (int o = 0; o < cout; ++o) o0[(v * cout + o) * hw + q] = acc[o];
+    // mapanything-rs/src/model.rs:155-168
+    const float nrm = fmaxf(sqrtf(acc[0] * acc[0] + acc[1] * acc[1] + acc[2] * acc[2]), 1e-8f);
+    const float depth = expf(acc[3]) * (scale ? *scale : 1.f);
+    if (o1) {
+      o1[px * 3 + 0] = acc[0] / nrm * depth;
+      o1[px * 3 + 1] = acc[1] / nrm * depth;
+      o1[px * 3 + 2] = acc[2] / nrm * depth;
+    }
+    if (o2) o2[px] = 1.f + expf(acc[4]);
+    if (o3) o3[px] = acc[5] > 0.f ? 1 : 0;
+  }
+}
+
 void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, int hw, int cin, int cout,
                     const float* w, const float* b, float* o0, float* o1, float* o2, uint8_t* o3, const float* scale) {
+  if ((cin == 32 || cin == 64 || cin == 128) && !ex.dry && pix > 0 && cout <= 8 &&
+      (reinterpret_cast<uintptr_t>(in) & 15) == 0) {
+    SPLAT_CHECK(mode != PW_DEPTH || cout == 2, BAD_ARGUMENT, "depth head has 2 channels");
+    SPLAT_CHECK(mode != PW_MA || cout == 6, BAD_ARGUMENT, "MapAnything head has 6 channels");
+    const double obytes = mode == PW_MA ? (o0 ? 24.0 : 0) + (o1 ? 12.0 : 0) + (o2 ? 4.0 : 0) + (o3 ? 1.0 : 0) : 4.0 * cout;
+    ProfScope ps(ex, "pointwise_head", 2.0 * pix * cin * cout, double(pix) * (cin * dtype_size(dt) + obytes));
+    const int lpp = cin / 8;
+    dim3 grid(cdiv(pix * lpp, 256));
+#define PWC(T, L) hipLaunchKernelGGL((pw_coop_kernel<T, L>), grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale)
+    if (dt == F32) {
+      if (lpp == 4) PWC(float, 4); else if (lpp == 8) PWC(float, 8); else PWC(float, 16);
+    } else {
+      if (lpp == 4) PWC(bf16, 4); else if (lpp == 8) PWC(bf16, 8); else PWC(bf16, 16);
+    }
+#undef PWC
+    SPLAT_HIP(hipGetLastError());
+    return;
+  }
   SPLAT_CHECK(cout <= 8 && cout * cin <= 8 * 256 && hw > 0, BAD_ARGUMENT, "pointwise_head sizes");
   SPLAT_CHECK(mode != PW_DEPTH || cout == 2, BAD_ARGUMENT, "depth head has 2 channels");
   SPLAT_CHECK(mode != PW_MA || cout == 6, BAD_ARGUMENT, "MapAnything head has 6 channels");
@@ -525,20 +746,25 @@ void swiglu_gate(const Exec& ex, int dt, const void* x12, int rows, int hidden, 
   SPLAT_HIP(hipGetLastError());
 }
 
+// Block (group, 64-column chunk): the 4 waves stride over the P rows, lanes over columns,
+// then the 4 partial sums meet in LDS.
 template <typename T>
 __global__ void mean_rows_kernel(const void* in, int groups, int P, int C, float* out) {
-  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= (long)groups * C) return;
-  const long gi = id / C, c = id % C;
+  __shared__ float part[4][64];
+  const int gi = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.y * 64 + lane;
   float s = 0.f;
-  for (int p = 0; p < P; ++p) s += ld<T>(in, (gi * P + p) * C + c);
-  out[id] = s / P;
+  if (c < C)
+    for (int p = wave; p < P; p += 4) s += ld<T>(in, ((long)gi * P + p) * C + c);
+  part[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < C) out[(long)gi * C + c] = (part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane]) / P;
 }
 
 void mean_rows(const Exec& ex, int dt, const void* in, int groups, int P, int C, float* out) {
   if (ex.dry) return;
   ProfScope ps(ex, "mean_rows", 0, double(groups) * P * C * dtype_size(dt) + 4.0 * groups * C);
-  dim3 grid(cdiv((long)groups * C, 256));
+  dim3 grid(groups, cdiv(C, 64));
   if (dt == F32) hipLaunchKernelGGL(mean_rows_kernel<float>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
   else hipLaunchKernelGGL(mean_rows_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
   SPLAT_HIP(hipGetLastError());
