@@ -234,7 +234,7 @@ def camera_head(p, camera_tokens):
     x = camera_tokens
     for name in ("backbone.0", "backbone.2"):
         x = F.relu(C.linear(x, p, f"{c}.{name}"))
-    x = x.float()
+    x = x if x.dtype == torch.float64 else x.float()   # output layers in f32 (camera_head.rs:67-68)
     return torch.cat([C.linear(x, p, c + ".fc_t"), C.linear(x, p, c + ".fc_qvec"),
                       F.relu(C.linear(x, p, c + ".fc_fov.0"))], 1)
 
