@@ -13,8 +13,10 @@
  * Tensors: images are [V, 3, H, W] float32, ImageNet-normalised, H and W multiples of 14.
  * Host-pointer entry points copy inputs in and outputs out and synchronise before
  * returning. *_device entry points take device pointers (HIP memory on the context's
- * device) and only enqueue on the context's stream (splat_stream); call
- * splat_synchronize or synchronise the stream before reading the outputs.
+ * device) and only enqueue on the context's stream (splat_stream); the caller orders the
+ * writes of the inputs before the call (e.g. an event on the producing stream waited on by
+ * splat_stream, or a device synchronisation), and calls splat_synchronize or synchronises
+ * the stream before reading the outputs.
  */
 #ifndef SPLATHIP_H
 #define SPLATHIP_H

@@ -12,6 +12,8 @@
 // column l%32.
 #include "kernels.h"
 
+#include <type_traits>
+
 namespace splat {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -87,6 +89,23 @@ __device__ inline void load8(const void* p, long i, bool f32, float* v) {
   }
 }
 
+// Store of 8 consecutive output values (16-byte aligned, all inside the output).
+template <typename T>
+__device__ inline void store8(const GemmArgs& p, const float* v, long idx) {
+  if (p.out_f32 || sizeof(T) == 4) {
+    float* o = reinterpret_cast<float*>(p.out) + idx;
+    *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint4 u;
+    u.x = pack_bf16x2(v[0], v[1]);
+    u.y = pack_bf16x2(v[2], v[3]);
+    u.z = pack_bf16x2(v[4], v[5]);
+    u.w = pack_bf16x2(v[6], v[7]);
+    *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p.out) + idx) = u;
+  }
+}
+
 // Epilogue of 8 consecutive columns n..n+7 of row m: bias, activation, table add, LayerScale,
 // residuals, store. `vec`: all of them exist and every operand is 16-byte aligned for them.
 template <typename T>
@@ -102,23 +121,7 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
     if (p.gamma) { load8(p.gamma, n, true, t); for (int k = 0; k < 8; ++k) v[k] *= t[k]; }
     if (p.res) { load8(p.res, row * p.ldres + n, rf, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
     if (p.res2) { load8(p.res2, row * p.ldres2 + n, rf2, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
-    const long idx = out_index(p, m, n, row);
-    if (p.out_f32) {
-      float* o = reinterpret_cast<float*>(p.out) + idx;
-      *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
-      *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
-    } else if (sizeof(T) == 4) {
-      float* o = reinterpret_cast<float*>(p.out) + idx;
-      *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
-      *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
-    } else {
-      uint4 u;
-      u.x = pack_bf16x2(v[0], v[1]);
-      u.y = pack_bf16x2(v[2], v[3]);
-      u.z = pack_bf16x2(v[4], v[5]);
-      u.w = pack_bf16x2(v[6], v[7]);
-      *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p.out) + idx) = u;
-    }
+    store8<T>(p, v, out_index(p, m, n, row));
     return;
   }
   for (int k = 0; k < 8; ++k) {
@@ -140,37 +143,124 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
 // Epilogue through LDS: each wave stages one 32-row slab of its accumulators at a time
 // (from the 32x32 accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4,
 // column l%32 of each 32x32 tile), then every lane finishes runs of 8 consecutive columns.
-// `slab` is this wave's LDS region of 32 x (TN*32 + 4) floats; the block must be past its
-// last read of the main-loop LDS.
-template <typename T, int TM, int TN>
-__device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long wrow0, long wcol0, float* slab,
-                                         int lane, bool vec) {
-  constexpr int COLS = TN * 32, LD = COLS + 4, RUNS = COLS / 8;
+// Three compile-time variants keep the code that a launch runs small (the unrolled slabs
+// multiply every optional feature, and instruction fetch, not memory, then bounds the
+// epilogue):
+//   EPI_BIAS  out = act(acc + bias)                          row-major, 16-byte runs
+//   EPI_RES   out = act(acc + bias) * gamma + res            row-major, 16-byte runs
+//   EPI_FULL  every feature (table add, row remap, second residual, transposed-conv
+//             scatter, unaligned or ragged runs) through epi8.
+// In the first two a lane always owns the same column run (RUNS divides 64), so bias and
+// LayerScale are loaded once, and the residuals of CH runs are requested before the first of
+// those runs is stored. `slab` is this wave's LDS region of 32 x slab_ld(TN) floats; the
+// block must be past its last read of the main-loop LDS.
+enum EpiKind { EPI_BIAS = 0, EPI_RES = 1, EPI_FULL = 2 };
+
+constexpr int slab_ld(int tn) { return tn * 32 + 4; }  // +4 floats: conflict-free 16-byte row reads
+
+template <int TM, int TN>
+__device__ __forceinline__ void stage_slab(const f32x16 (&acc)[TM][TN], int i, float* slab, int lane) {
+  constexpr int LD = slab_ld(TN);
   const int g = lane >> 5, l32 = lane & 31;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+  for (int j = 0; j < TN; ++j)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+    for (int r = 0; r < 16; ++r) slab[(8 * (r >> 2) + 4 * g + (r & 3)) * LD + j * 32 + l32] = acc[i][j][r];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void slab_done() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void read8(const float* q, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(q);
+  const float4 b = *reinterpret_cast<const float4*>(q + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <typename T, int TM, int TN, int EPI>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long wrow0, long wcol0, float* slab,
+                                         int lane, bool vec) {
+  constexpr int COLS = TN * 32, LD = slab_ld(TN), RUNS = COLS / 8;
+  if constexpr (EPI == EPI_FULL) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) slab[(8 * (r >> 2) + 4 * g + (r & 3)) * LD + j * 32 + l32] = acc[i][j][r];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int q = lane; q < 32 * RUNS; q += 64) {
-      const int rr = q / RUNS, cc = (q - rr * RUNS) * 8;
-      const long m = wrow0 + i * 32 + rr, n = wcol0 + cc;
-      if (m < p.M && n < p.N) {
-        float v[8];
-        const float4 a = *reinterpret_cast<const float4*>(slab + rr * LD + cc);
-        const float4 b = *reinterpret_cast<const float4*>(slab + rr * LD + cc + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        epi8<T>(p, v, m, n, vec && n + 8 <= p.N);
+    for (int i = 0; i < TM; ++i) {
+      stage_slab<TM, TN>(acc, i, slab, lane);
+      for (int q = lane; q < 32 * RUNS; q += 64) {
+        const int rr = q / RUNS, cc = (q - rr * RUNS) * 8;
+        const long m = wrow0 + i * 32 + rr, n = wcol0 + cc;
+        if (m < p.M && n < p.N) {
+          float v[8];
+          read8(slab + rr * LD + cc, v);
+          epi8<T>(p, v, m, n, vec && n + 8 <= p.N);
+        }
       }
+      slab_done();
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    constexpr int IT = 32 * RUNS / 64;   // runs per lane per slab
+    constexpr int CH = IT < 4 ? IT : 4;  // runs whose residual loads are in flight together
+    static_assert(64 % RUNS == 0 && IT % CH == 0, "run layout");
+    const int cc = (lane % RUNS) * 8, rsub = lane / RUNS;
+    const long n = wcol0 + cc;
+    const bool nok = n < p.N;  // the host guarantees that a run starting inside the output lies in it
+    float cb[8], cg[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) { cb[k] = 0.f; cg[k] = 1.f; }
+    if (nok && p.bias) load8(p.bias, n, true, cb);
+    if (EPI == EPI_RES && nok && p.gamma) load8(p.gamma, n, true, cg);
+    const bool rf = p.res_f32 || sizeof(T) == 4;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      stage_slab<TM, TN>(acc, i, slab, lane);
+#pragma unroll
+      for (int t0 = 0; t0 < IT; t0 += CH) {
+        float v[CH][8], rv[CH][8];
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+          const int rr = rsub + (t0 + t) * (64 / RUNS);
+          const long m = wrow0 + i * 32 + rr;
+          read8(slab + rr * LD + cc, v[t]);
+          if (EPI == EPI_RES && p.res && nok && m < p.M) load8(p.res, m * p.ldres + n, rf, rv[t]);
+        }
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+          const long m = wrow0 + i * 32 + rsub + (t0 + t) * (64 / RUNS);
+          float* x = v[t];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) x[k] += cb[k];
+          if (p.act == ACT_RELU) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] = fmaxf(x[k], 0.f);
+          } else if (p.act == ACT_GELU) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] = gelu_erf(x[k]);
+          }
+          if (EPI == EPI_RES) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] *= cg[k];
+            if (p.res) {
+#pragma unroll
+              for (int k = 0; k < 8; ++k) x[k] += rv[t][k];
+            }
+          }
+          if (nok && m < p.M) store8<T>(p, x, m * p.ldc + n);
+        }
+      }
+      slab_done();
+    }
   }
+}
+
+// Which epilogue variant a launch needs (host side; `a.epi_vec` already set).
+inline int epi_kind(const GemmArgs& a) {
+  if (!a.epi_vec || a.rm_P || a.store != STORE_ROWS || a.addtab || a.res2) return EPI_FULL;
+  return (a.res || a.gamma) ? EPI_RES : EPI_BIAS;
 }
 
 // Whether the 8-column vector path is valid for every run of a launch (host side).
@@ -195,6 +285,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs p) {
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   constexpr int ACH = BM / 32, BCH = BN / 32;  // 16-byte chunks per thread per tile
   __shared__ __attribute__((aligned(16))) char smem[2 * (BM + BN) * LDS_ROW];
+  static_assert(2 * (BM + BN) * LDS_ROW >= 4 * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the tiles");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -303,19 +394,20 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs p) {
     __syncthreads();
   }
 
-  float* slab = reinterpret_cast<float*>(smem) + wave * 32 * (TN * 32 + 4);
-  epilogue<T, TM, TN>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec);
+  float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
+  epilogue<T, TM, TN, EPI_FULL>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec);
 }
 
 // ---------------------------------------------------------------------------------------
 // bf16 main path. Operand tiles stream from global memory straight into LDS through a
 // STAGES-deep ring (buffer_load_dwordx4 ... lds: 16 bytes per lane, one wave instruction fills
-// 1 KB = 8 tile rows of 128 bytes), so no registers stage them, and rows or K-chunks outside
-// the operands read as zero through the buffer descriptor's range check (offset 0x80000000).
-// Chunk c (16 bytes) of tile row r sits in slot c ^ ((r >> 1) & 7): the 16-lane phases of the
-// fragment reads (16 consecutive rows, one chunk) then touch 16 distinct 4-bank groups. The
-// loads are inline asm so that the compiler adds no waits of its own; the pipeline waits with
-// explicit vmcnt counts and one barrier per k-tile.
+// 1 KB = 8 tile rows of 128 bytes at BK=64), so no registers stage them, and rows or K-chunks
+// outside the operands read as zero through the buffer descriptor's range check (offset
+// 0x80000000). Chunk c (16 bytes) of tile row r sits in slot c ^ ((r >> 1) & 7): the 16-lane
+// phases of the fragment reads (16 consecutive rows, one chunk) then touch 16 distinct 4-bank
+// groups. The loads are inline asm so that the compiler adds no waits of its own; the pipeline
+// waits with explicit vmcnt counts and one barrier per k-tile, placed before the tile's last
+// k-step so that the first fragments of the next tile are read while that step's MFMAs run.
 
 typedef int int32x4_t __attribute__((ext_vector_type(4)));
 
@@ -345,13 +437,19 @@ template <int N> __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt v
 
 constexpr uint32_t OOB = 0x80000000u;
 
-template <int BM, int BN, int WM, int WN, int STAGES, int AMODE, bool RELU>
+template <int BM, int BN, int WM, int WN, int STAGES, int BK, int AMODE, bool RELU, int EPI>
 __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-  constexpr int AL = BM / 32, BL = BN / 32;  // load instructions per wave per k-tile
+  // A tile row holds BK bf16 = RB bytes = CPR 16-byte chunks; one load instruction of a wave
+  // fills RPI rows (1 KiB). Chunk c of row r sits in slot c ^ ((r >> SH) & (CPR - 1)), which
+  // keeps the 16 lanes of every ds_read_b128 phase on distinct banks.
+  constexpr int RB = BK * 2, CPR = RB / 16, RPI = 64 / CPR, SH = CPR == 8 ? 1 : 2, KS = BK / 16;
+  static_assert(BK == 64 || BK == 32, "k-tile");
+  constexpr int AL = BM / (4 * RPI), BL = BN / (4 * RPI);  // load instructions per wave per k-tile
   constexpr int LPT = AL + BL;
-  constexpr int STAGE = (BM + BN) * 128;
-  static_assert((STAGES - 2) * LPT <= 63, "vmcnt range");
+  constexpr int STAGE = (BM + BN) * RB;
+  static_assert((STAGES - 1) * LPT <= 63, "vmcnt range");
+  static_assert(STAGES * STAGE >= 4 * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the ring");
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -370,15 +468,15 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
   const int tn = (bid % per_group) / gsize;
   const long m0 = long(tm) * BM, n0 = long(tn) * BN;
 
-  // Each lane loads chunk c of tile row r = (i*4 + wave)*8 + lane/8 for instruction i; with
-  // slot lane%8 that chunk is slot ^ ((r >> 1) & 7), the same for every i.
-  const int lrow = lane >> 3;
-  const int c = (lane & 7) ^ ((4 * (wave & 1) + (lrow >> 1)) & 7);
+  // Each lane loads chunk c of tile row r = (i*4 + wave)*RPI + lane/CPR for instruction i; with
+  // slot lane%CPR that chunk is slot ^ ((r >> SH) & (CPR-1)), the same for every i.
+  const int lrow = lane / CPR;
+  const int c = (lane % CPR) ^ (((wave * RPI + lrow) >> SH) & (CPR - 1));
   const int32x4_t rw = make_rsrc(p.W, uint32_t(long(p.N) * p.ldw * 2));
   uint32_t boff[BL];
 #pragma unroll
   for (int i = 0; i < BL; ++i) {
-    const long n = n0 + (i * 4 + wave) * 8 + lrow;
+    const long n = n0 + (i * 4 + wave) * RPI + lrow;
     boff[i] = n < p.N ? uint32_t(n * p.ldw * 2 + c * 16) : OOB;
   }
   int32x4_t ra;
@@ -388,7 +486,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
     ra = make_rsrc(p.A, uint32_t(long(p.M) * p.lda * 2));
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
-      const long m = m0 + (i * 4 + wave) * 8 + lrow;
+      const long m = m0 + (i * 4 + wave) * RPI + lrow;
       aoff[i] = m < p.M ? uint32_t(m * p.lda * 2 + c * 16) : OOB;
     }
   } else {
@@ -396,7 +494,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
     const int hw = p.Ho * p.Wo;
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
-      const long m = m0 + (i * 4 + wave) * 8 + lrow;
+      const long m = m0 + (i * 4 + wave) * RPI + lrow;
       if (m < p.M) {
         const int v = int(m / hw), rem = int(m - long(v) * hw);
         const int oy = rem / p.Wo, ox = rem - oy * p.Wo;
@@ -413,12 +511,12 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
 
   auto issue = [&](int kt, int stage) {
     const uint32_t sb = lds_addr(smem + stage * STAGE);
-    const int k = kt * 64 + c * 8;
+    const int k = kt * BK + c * 8;
     if (AMODE == A_ROWS) {
       const bool kin = k < p.K;
 #pragma unroll
       for (int i = 0; i < AL; ++i)
-        load_to_lds(ra, (kin && aoff[i] != OOB) ? aoff[i] + kt * 128 : OOB, sb + (i * 4 + wave) * 1024);
+        load_to_lds(ra, (kin && aoff[i] != OOB) ? aoff[i] + kt * RB : OOB, sb + (i * 4 + wave) * 1024);
     } else {
       const int tap = k / p.Cin, ci = k - tap * p.Cin;
       const int ky = tap / p.ks, kx = tap - ky * p.ks;
@@ -432,7 +530,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
     }
 #pragma unroll
     for (int i = 0; i < BL; ++i)
-      load_to_lds(rw, boff[i] != OOB ? boff[i] + kt * 128 : OOB, sb + BM * 128 + (i * 4 + wave) * 1024);
+      load_to_lds(rw, boff[i] != OOB ? boff[i] + kt * RB : OOB, sb + BM * RB + (i * 4 + wave) * 1024);
   };
 
   f32x16 acc[TM][TN];
@@ -443,51 +541,93 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int sw = (l32 >> 1) & 7;
-  const int arow0 = (wm * (BM / WM) + l32) * 128, brow0 = (BM + wn * (BN / WN) + l32) * 128;
-  const int nk = (p.K + 63) / 64;
+  const int sw = (l32 >> SH) & (CPR - 1);  // fragment rows are l32 plus multiples of 32
+  const int arow0 = (wm * (BM / WM) + l32) * RB, brow0 = (BM + wn * (BN / WN) + l32) * RB;
+  const int nk = (p.K + BK - 1) / BK;
+  // Prologue: STAGES tiles in flight, tile 0 resident for every wave, its first fragments read.
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
+  for (int s = 0; s < STAGES; ++s)
     if (s < nk) issue(s, s);
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * LPT>();
-    else wait_vmcnt<0>();
-    __syncthreads();
-    if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+  if (STAGES - 1 < nk) wait_vmcnt<(STAGES - 1) * LPT>();
+  else wait_vmcnt<0>();
+  __syncthreads();
+  // Fragments of the next k-step (of this tile, or step 0 of the next tile) are read while the
+  // matrix cores work on the current one.
+  uint4 fa[2][TM], fb[2][TN];
+  auto read_frags = [&](const char* sb, int s, int slot) {
+    const int off = ((2 * s + g) ^ sw) * 16;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[slot][i] = *reinterpret_cast<const uint4*>(sb + arow0 + i * 32 * RB + off);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[slot][j] = *reinterpret_cast<const uint4*>(sb + brow0 + j * 32 * RB + off);
+  };
+  read_frags(smem, 0, 0);
+  // One k-tile; the last one is peeled (HAS_NEXT false) so that each step's reads and MFMAs
+  // share a basic block and the LDS waits stay exact.
+  auto tile = [&](int kt, auto has_next) {
+    constexpr bool HAS_NEXT = decltype(has_next)::value;
     const char* sb = smem + (kt % STAGES) * STAGE;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int off = ((2 * s + g) ^ sw) * 16;
-      uint4 fa[TM], fb[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const uint4*>(sb + arow0 + i * 32 * 128 + off);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const uint4*>(sb + brow0 + j * 32 * 128 + off);
+    for (int s = 0; s < KS; ++s) {
+      // hard fence: the reads below belong to this step's region and nothing moves across
+      __builtin_amdgcn_sched_barrier(0);
+      const bool reads = s + 1 < KS || HAS_NEXT;
+      if (s + 1 < KS) {
+        read_frags(sb, s + 1, (s + 1) & 1);
+      } else if constexpr (HAS_NEXT) {
+        // Every wave holds its last fragments of tile kt (the barrier waits for LDS reads), so
+        // the stage of tile kt can take tile kt+STAGES; tile kt+1 must be resident first.
+        if (kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * LPT>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        if (kt + STAGES < nk) issue(kt + STAGES, kt % STAGES);
+        read_frags(smem + ((kt + 1) % STAGES) * STAGE, 0, 0);
+      }
       if (RELU) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa[i] = Mfma<bf16>::relu(fa[i]);
+        for (int i = 0; i < TM; ++i) fa[s & 1][i] = Mfma<bf16>::relu(fa[s & 1][i]);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) Mfma<bf16>::mma(acc[i][j], fa[i], fb[j]);
+        for (int j = 0; j < TN; ++j) Mfma<bf16>::mma(acc[i][j], fa[s & 1][i], fb[s & 1][j]);
+      if (reads) {
+        // interleave the LDS reads with this step's MFMAs
+#pragma unroll
+        for (int k = 0; k < TM + TN; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, TM * TN / (TM + TN) > 0 ? TM * TN / (TM + TN) : 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-  }
+  };
+  for (int kt = 0; kt + 1 < nk; ++kt) tile(kt, std::true_type{});
+  tile(nk - 1, std::false_type{});
   __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
-  float* slab = reinterpret_cast<float*>(smem) + wave * 32 * (TN * 32 + 4);
-  epilogue<bf16, TM, TN>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec);
+  float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
+  epilogue<bf16, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec);
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES>
+template <int BM, int BN, int WM, int WN, int STAGES, int BK = 64>
 static void launch_bf16(const Exec& ex, const GemmArgs& a) {
   const int tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
   dim3 grid(tm * tn);
-  if (a.amode == A_ROWS)
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, A_ROWS, false>), grid, dim3(256), 0, ex.stream, a, tm, tn);
-  else if (!a.relu_in)
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, A_CONV, false>), grid, dim3(256), 0, ex.stream, a, tm, tn);
-  else
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, A_CONV, true>), grid, dim3(256), 0, ex.stream, a, tm, tn);
+  const int epi = epi_kind(a);
+#define SPLAT_GO(AM, RL, EP) \
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(256), 0, ex.stream, a, tm, tn)
+  if (a.amode == A_ROWS) {
+    if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
+    else if (epi == EPI_RES) SPLAT_GO(A_ROWS, false, EPI_RES);
+    else SPLAT_GO(A_ROWS, false, EPI_FULL);
+  } else if (epi == EPI_BIAS) {
+    if (a.relu_in) SPLAT_GO(A_CONV, true, EPI_BIAS);
+    else SPLAT_GO(A_CONV, false, EPI_BIAS);
+  } else {
+    if (a.relu_in) SPLAT_GO(A_CONV, true, EPI_FULL);
+    else SPLAT_GO(A_CONV, false, EPI_FULL);
+  }
+#undef SPLAT_GO
   SPLAT_HIP(hipGetLastError());
 }
 

@@ -43,6 +43,7 @@ def test_gemm_matches_torch(ctx, dtype, M, N, K, act):
     bias = torch.randn(N, generator=g)
     dA, dW, db = A.cuda(), Wm.cuda(), bias.cuda()
     out = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()  # inputs were written on torch's stream, the library runs on its own
     ctx.kernel_gemm(code, dA.data_ptr(), M, K, dW.data_ptr(), N, ldw, db.data_ptr(), act, out.data_ptr(), True)
     ctx.synchronize()
     ref = A.double() @ Wm[:, :K].double().T + bias.double()
@@ -56,6 +57,7 @@ def test_gemm_matches_torch(ctx, dtype, M, N, K, act):
     assert err < (1e-5 if dtype == "f32" else 2e-5), err
     # bf16/fp32 output storage path
     out2 = torch.empty(M, N, dtype=tdt, device="cuda")
+    torch.cuda.synchronize()  # inputs were written on torch's stream, the library runs on its own
     ctx.kernel_gemm(code, dA.data_ptr(), M, K, dW.data_ptr(), N, ldw, db.data_ptr(), act, out2.data_ptr(), False)
     ctx.synchronize()
     err2 = (out2.cpu().double() - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
@@ -84,6 +86,7 @@ def test_attention_matches_torch(ctx, dtype, S, L, heads):
     qkv = (torch.randn(S * L, 3 * heads * 64, generator=g) * 1.5).to(tdt)
     dq = qkv.cuda()
     out = torch.empty(S * L, heads * 64, dtype=tdt, device="cuda")
+    torch.cuda.synchronize()  # inputs were written on torch's stream, the library runs on its own
     ctx.kernel_attention(code, dq.data_ptr(), out.data_ptr(), S, L, heads)
     ctx.synchronize()
     x = dq.double().reshape(S, L, 3, heads, 64).permute(2, 0, 3, 1, 4)  # [3, S, h, L, 64]
@@ -136,6 +139,7 @@ def test_conv2d_matches_torch(ctx, dtype, V, H, W, Cin, Cout, ks, stride, relu_i
     dres = res.permute(0, 2, 3, 1).contiguous().cuda() if residual else None
     out = torch.empty(V, Ho, Wo, Cout, dtype=tdt, device="cuda")
     dw, db = wp.cuda(), b.cuda()
+    torch.cuda.synchronize()  # inputs were written on torch's stream, the library runs on its own
     ctx.kernel_conv2d(code, dx.data_ptr(), V, H, W, Cin, dw.data_ptr(), Cout, ldw, ks, stride, db.data_ptr(),
                       relu_in, act, dres.data_ptr() if residual else 0, out.data_ptr())
     ctx.synchronize()
@@ -162,6 +166,7 @@ def test_conv_transpose2d_matches_torch(ctx, dtype, V, R, Cc, Cin, Cout, s):
     dx = x.permute(0, 2, 3, 1).contiguous().cuda()
     out = torch.empty(V, R * s, Cc * s, Cout, dtype=tdt, device="cuda")
     dw, db = wp.cuda(), bx.cuda()
+    torch.cuda.synchronize()  # inputs were written on torch's stream, the library runs on its own
     ctx.kernel_conv_transpose2d(code, dx.data_ptr(), V, R, Cc, Cin, dw.data_ptr(), Cout, ldw, s, db.data_ptr(),
                                 out.data_ptr())
     ctx.synchronize()
@@ -181,6 +186,7 @@ def test_resize_bilinear_matches_torch(ctx, dtype, V, Hi, Wi, C, Ho, Wo):
     ref = torch.nn.functional.interpolate(x.double(), size=(Ho, Wo), mode="bilinear", align_corners=True)
     dx = x.permute(0, 2, 3, 1).contiguous().cuda()
     out = torch.empty(V, Ho, Wo, C, dtype=tdt, device="cuda")
+    torch.cuda.synchronize()  # inputs were written on torch's stream, the library runs on its own
     ctx.kernel_resize_bilinear(code, dx.data_ptr(), V, Hi, Wi, C, out.data_ptr(), Ho, Wo)
     ctx.synchronize()
     got = out.cpu().double().permute(0, 3, 1, 2)
