@@ -430,7 +430,7 @@ __device__ inline uint32_t lds_addr(const void* p) {
 __device__ inline void load_to_lds(const int32x4_t& rsrc, uint32_t voffset, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(__builtin_amdgcn_readfirstlane(int(lds))),
                "v"(voffset), "s"(rsrc)
-               : "memory");
+               : "memory");  // m0 is set here and used by nothing else in these kernels
 }
 
 template <int N> __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
@@ -509,28 +509,27 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
     }
   }
 
-  auto issue = [&](int kt, int stage) {
+  // Load instruction l (l < AL: A rows, else W rows) of k-tile kt into ring stage `stage`.
+  // K-chunks at or past K (tail and tiles beyond the last) read as zeros.
+  auto issue_one = [&](int kt, int stage, int l) {
     const uint32_t sb = lds_addr(smem + stage * STAGE);
     const int k = kt * BK + c * 8;
-    if (AMODE == A_ROWS) {
-      const bool kin = k < p.K;
-#pragma unroll
-      for (int i = 0; i < AL; ++i)
+    const bool kin = k < p.K;
+    if (l < AL) {
+      const int i = l;
+      if (AMODE == A_ROWS) {
         load_to_lds(ra, (kin && aoff[i] != OOB) ? aoff[i] + kt * RB : OOB, sb + (i * 4 + wave) * 1024);
-    } else {
-      const int tap = k / p.Cin, ci = k - tap * p.Cin;
-      const int ky = tap / p.ks, kx = tap - ky * p.ks;
-      const bool kin = k < p.K;
-#pragma unroll
-      for (int i = 0; i < AL; ++i) {
+      } else {
+        const int tap = k / p.Cin, ci = k - tap * p.Cin;
+        const int ky = tap / p.ks, kx = tap - ky * p.ks;
         const int iy = aiy[i] + ky, ix = aix[i] + kx;
         const bool ok = kin && iy >= 0 && iy < p.Hi && ix >= 0 && ix < p.Wi;
         load_to_lds(ra, ok ? aoff[i] + uint32_t((iy * p.Wi + ix) * p.Cin + ci) * 2 : OOB, sb + (i * 4 + wave) * 1024);
       }
+    } else {
+      const int i = l - AL;
+      load_to_lds(rw, (kin && boff[i] != OOB) ? boff[i] + kt * RB : OOB, sb + BM * RB + (i * 4 + wave) * 1024);
     }
-#pragma unroll
-    for (int i = 0; i < BL; ++i)
-      load_to_lds(rw, boff[i] != OOB ? boff[i] + kt * RB : OOB, sb + BM * RB + (i * 4 + wave) * 1024);
   };
 
   f32x16 acc[TM][TN];
@@ -545,11 +544,13 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
   const int arow0 = (wm * (BM / WM) + l32) * RB, brow0 = (BM + wn * (BN / WN) + l32) * RB;
   const int nk = (p.K + BK - 1) / BK;
   // Prologue: STAGES tiles in flight, tile 0 resident for every wave, its first fragments read.
+  // Every k-tile slot is loaded, also past the last tile (as zeros), so that the number of
+  // loads in flight, and with it each vmcnt wait, is the same for every tile.
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
-    if (s < nk) issue(s, s);
-  if (STAGES - 1 < nk) wait_vmcnt<(STAGES - 1) * LPT>();
-  else wait_vmcnt<0>();
+#pragma unroll
+    for (int l = 0; l < LPT; ++l) issue_one(s, s, l);
+  wait_vmcnt<(STAGES - 1) * LPT>();
   __syncthreads();
   // Fragments of the next k-step (of this tile, or step 0 of the next tile) are read while the
   // matrix cores work on the current one.
@@ -564,6 +565,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
   read_frags(smem, 0, 0);
   // One k-tile; the last one is peeled (HAS_NEXT false) so that each step's reads and MFMAs
   // share a basic block and the LDS waits stay exact.
+  constexpr int MM = TM * TN, NF = TM + TN, CUR = (KS - 1) & 1;
   auto tile = [&](int kt, auto has_next) {
     constexpr bool HAS_NEXT = decltype(has_next)::value;
     const char* sb = smem + (kt % STAGES) * STAGE;
@@ -571,32 +573,45 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
     for (int s = 0; s < KS; ++s) {
       // hard fence: the reads below belong to this step's region and nothing moves across
       __builtin_amdgcn_sched_barrier(0);
-      const bool reads = s + 1 < KS || HAS_NEXT;
-      if (s + 1 < KS) {
-        read_frags(sb, s + 1, (s + 1) & 1);
-      } else if constexpr (HAS_NEXT) {
-        // Every wave holds its last fragments of tile kt (the barrier waits for LDS reads), so
-        // the stage of tile kt can take tile kt+STAGES; tile kt+1 must be resident first.
-        if (kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * LPT>();
-        else wait_vmcnt<0>();
-        __syncthreads();
-        if (kt + STAGES < nk) issue(kt + STAGES, kt % STAGES);
-        read_frags(smem + ((kt + 1) % STAGES) * STAGE, 0, 0);
-      }
       if (RELU) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) fa[s & 1][i] = Mfma<bf16>::relu(fa[s & 1][i]);
       }
+      if (s + 1 < KS || !HAS_NEXT) {
+        if (s + 1 < KS) read_frags(sb, s + 1, (s + 1) & 1);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) Mfma<bf16>::mma(acc[i][j], fa[s & 1][i], fb[s & 1][j]);
-      if (reads) {
-        // interleave the LDS reads with this step's MFMAs
+          for (int j = 0; j < TN; ++j) Mfma<bf16>::mma(acc[i][j], fa[s & 1][i], fb[s & 1][j]);
+        if (s + 1 < KS) {
+          // interleave the LDS reads with this step's MFMAs
 #pragma unroll
-        for (int k = 0; k < TM + TN; ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x008, TM * TN / (TM + TN) > 0 ? TM * TN / (TM + TN) : 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          for (int k = 0; k < NF; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, MM / NF > 0 ? MM / NF : 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+        }
+      } else {
+        // Last step of a tile with a successor. Every wave holds its last fragments of tile kt
+        // (the barrier waits for LDS reads), so the stage of tile kt takes tile kt+STAGES, once
+        // tile kt+1 is resident. The loads of tile kt+STAGES and the reads of the next tile's
+        // first fragments are spread between this step's MFMAs, in a fixed order, so that the
+        // load queue never fills up in front of the matrix core.
+        wait_vmcnt<(STAGES - 2) * LPT>();
+        __syncthreads();
+        const char* nb = smem + ((kt + 1) % STAGES) * STAGE;
+        const int off0 = (g ^ sw) * 16;
+#pragma unroll
+        for (int q = 0; q < MM; ++q) {
+          Mfma<bf16>::mma(acc[q / TN][q % TN], fa[CUR][q / TN], fb[CUR][q % TN]);
+#pragma unroll
+          for (int l = q * LPT / MM; l < (q + 1) * LPT / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l);
+#pragma unroll
+          for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) {
+            if (r < TM) fa[0][r] = *reinterpret_cast<const uint4*>(nb + arow0 + r * 32 * RB + off0);
+            else fb[0][r - TM] = *reinterpret_cast<const uint4*>(nb + brow0 + (r - TM) * 32 * RB + off0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -604,6 +619,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
   };
   for (int kt = 0; kt + 1 < nk; ++kt) tile(kt, std::true_type{});
   tile(nk - 1, std::false_type{});
+  wait_vmcnt<0>();  // the zero-fill loads past the last tile must land before the ring is reused
   __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
   float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
   epilogue<bf16, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec);
