@@ -24,6 +24,20 @@ for p in (ROOT, os.path.join(ROOT, "splatting-rs_amd")):
 PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}   # dense MFMA, MI355X
 PEAK_HBM_GBS = 8000.0
 MFMA_KERNELS = ("gemm", "conv_igemm", "attention")
+COPY_CAL_BYTES = 256 << 20
+# HBM bytes per launch of a kernel class, from FETCH_SIZE / WRITE_SIZE counter runs of this
+# script (each scaled by the same counter on the --copy-calibration kernel); written next to
+# the rocprofv3 summaries it comes from.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def measured_traffic(cfg_key, kernel):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f).get(cfg_key, {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return rec["bytes_per_launch"] if rec else None
 
 
 def log(*a):
@@ -126,6 +140,9 @@ def main():
     ap.add_argument("--no-graphs", action="store_true", help="eager launches instead of HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-out", default="", help="write the per-kernel-class profile as JSON here")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 256 MiB -> 256 MiB streaming kernel (torch.neg on fp32), the "
+                         "reference that scales FETCH_SIZE / WRITE_SIZE counter runs to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the network would "
@@ -139,6 +156,13 @@ def main():
     from splathip import specs, synth
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calibration:
+        src = torch.ones(COPY_CAL_BYTES // 4, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     cfg = specs.CONFIGS[args.config]
     ctx = splathip.Context(0)
     with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
@@ -185,7 +209,7 @@ def main():
         achieved = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
     roof["frac"] = roof["achieved"] / roof["peak"]
-    roof["traffic"] = None
+    roof["traffic"] = measured_traffic(cfg.key, dom["name"])
     roof["kernel"] = dom["name"]
     roof["launches_per_forward"] = dom["launches"]
     roof["avg_launch_us"] = 1e3 * dom["ms"] / dom["launches"]

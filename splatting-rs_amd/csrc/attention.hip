@@ -286,12 +286,16 @@ __global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p,
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int h = blockIdx.y;
   const int L = p.L;
-  const long base = long(blockIdx.z) * p.seq_stride;
+  // 1D grid over (query block, head, sequence), query blocks fastest; the query blocks of one
+  // head, which all stream the same K and V, run on one XCD.
+  const int nq = (L + WAVES * QT * 32 - 1) / (WAVES * QT * 32);
+  const int id = xcd_contiguous(blockIdx.x, nq * p.heads * p.seqs);
+  const int qb = id % nq, h = (id / nq) % p.heads, sq = id / (nq * p.heads);
+  const long base = long(sq) * p.seq_stride;
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + h * 64;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + h * 64;
-  const int q0 = (blockIdx.x * WAVES + wave) * (QT * 32);
+  const int q0 = (qb * WAVES + wave) * (QT * 32);
 
   uint4 qf[QT][4];
 #pragma unroll
@@ -496,7 +500,7 @@ void attention(const Exec& ex, const AttnArgs& a) {
   } else if (long(a.L) * a.ld * 2 < 2147483648L && a.ld % 8 == 0 && a.ldo % 4 == 0) {
     // 4 waves x 32 queries: two sub-tiles of queries per wave (QT = 2) measured slower on
     // gfx950 (register pressure pushes the accumulators through AGPR moves).
-    hipLaunchKernelGGL((attn_bf16_kernel<4, 1>), dim3(cdiv(a.L, 128), a.heads, a.seqs), dim3(256), 0, ex.stream, a, c);
+    hipLaunchKernelGGL((attn_bf16_kernel<4, 1>), dim3(cdiv(a.L, 128) * a.heads * a.seqs), dim3(256), 0, ex.stream, a, c);
   } else {
     dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
     hipLaunchKernelGGL(attn_kernel<bf16>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);

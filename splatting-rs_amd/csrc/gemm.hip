@@ -456,11 +456,13 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
   const int wm = wave / WN, wn = wave % WN;
   const int g = lane >> 5, l32 = lane & 31;
 
-  // Tile order: blocks b, b+8, ... land on one XCD; give each XCD a contiguous run of tiles,
-  // walked in groups of 8 tile rows so that neighbours share A and W panels in its L2.
+  // Tile order, walked in groups of 8 tile rows so that neighbouring tiles share A and W
+  // panels. Blocks b, b+8, ... land on one XCD (round-robin dispatch): when the tile count is a
+  // multiple of 8 each XCD takes a contiguous run of tiles (8192^3: 1.30 vs 1.01 PFLOP/s
+  // dealt round-robin); otherwise the round-robin deal, which keeps one tile row per XCD and
+  // measured the same time and less HBM traffic than contiguous runs on the network's shapes.
   const int nblk = tiles_m * tiles_n;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int bid = (nblk & 7) == 0 ? xcd_contiguous(blockIdx.x, nblk) : blockIdx.x;
   const int per_group = 8 * tiles_n;
   const int first_m = (bid / per_group) * 8;
   const int gsize = min(tiles_m - first_m, 8);
