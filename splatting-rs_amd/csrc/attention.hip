@@ -274,15 +274,21 @@ template <int N> __device__ inline void wait_vm() { asm volatile("s_waitcnt vmcn
 }  // namespace
 
 template <int WAVES, int QT>
-__global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p, float c) {
+__global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs p, float c) {
   constexpr int NT = WAVES * 64;
   constexpr int KBYTES = 64 * 128;            // K tile: 64 keys x 128 bytes, swizzled, unpadded
-  constexpr int VROW = 64 * 2 + 8;            // V^T row: 64 keys (bf16) + pad
+  // V^T row: 64 keys (bf16) + 16 bytes (16-byte aligned rows, conflict-free 16-lane reads).
+  // Within every 16 keys the 4-key quads are stored in the order 0, 2, 1, 3, so that the 8
+  // keys one lane feeds the matrix core (quads g and g+2 of the 16) are 16 contiguous bytes.
+  constexpr int VROW = 64 * 2 + 16;
   constexpr int VBYTES = 64 * VROW;
   constexpr int KL = 8 / WAVES;               // K load instructions per wave per tile
   constexpr int VB = 256 / NT;                // 4x4 V blocks per thread per tile
   static_assert(WAVES == 2 || WAVES == 4, "the K-load swizzle assumes an even number of waves");
-  __shared__ __attribute__((aligned(1024))) char smem[2 * (KBYTES + VBYTES)];
+  // LDS: two K tiles and two V^T tiles. K and V of tile t+1 are requested when tile t starts
+  // (V into registers, stored transposed when tile t is done). A deeper K ring measured no
+  // faster: the loop is bound by its VALU work, not by load latency.
+  __shared__ __attribute__((aligned(1024))) char smem[2 * KBYTES + 2 * VBYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -313,7 +319,7 @@ __global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p,
   const int lrow = lane >> 3;
   const int kc = (lane & 7) ^ ((4 * (wave & 1) + (lrow >> 1)) & 7);
   auto issue_k = [&](int t, int buf) {
-    const uint32_t sb = uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_a)(smem + buf * (KBYTES + VBYTES))));
+    const uint32_t sb = uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_a)(smem + buf * KBYTES)));
 #pragma unroll
     for (int i = 0; i < KL; ++i) {
       const int row = (i * WAVES + wave) * 8 + lrow;
@@ -321,20 +327,34 @@ __global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p,
       load_lds_a(rk, key < L ? uint32_t(key * p.ld * 2 + kc * 16) : 0x80000000u, sb + (i * WAVES + wave) * 1024);
     }
   };
+  // V rows through a buffer descriptor too: every load is issued (rows past the sequence read
+  // as zero), so the number of loads per tile, and with it each vmcnt wait, is fixed.
+  const __amdgpu_buffer_rsrc_t rvs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(V + base * p.ld), 0, int(long(L) * p.ld * 2), 0x00020000);
   uint2 rv[VB][4];
+  int voff[VB][4];  // byte offset of this thread's V rows within a tile
+#pragma unroll
+  for (int b = 0; b < VB; ++b)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int blk = tid + b * NT, kq = blk >> 4, dq = blk & 15;
+      voff[b][j] = ((4 * kq + j) * p.ld + 4 * dq) * 2;
+    }
   auto load_v = [&](int t) {
+    const int tile_off = t * 64 * p.ld * 2;
 #pragma unroll
     for (int b = 0; b < VB; ++b) {
-      const int blk = tid + b * NT, kq = blk >> 4, dq = blk & 15;
+      const int kq = (tid + b * NT) >> 4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = t * 64 + 4 * kq + j;
-        rv[b][j] = key < L ? *reinterpret_cast<const uint2*>(V + (base + key) * p.ld + 4 * dq) : make_uint2(0, 0);
+        const auto w = __builtin_amdgcn_raw_buffer_load_b64(rvs, key < L ? tile_off + voff[b][j] : int(0x80000000u), 0, 0);
+        rv[b][j] = make_uint2(w[0], w[1]);
       }
     }
   };
   auto store_v = [&](int buf) {
-    char* vt = smem + buf * (KBYTES + VBYTES) + KBYTES;
+    char* vt = smem + 2 * KBYTES + buf * VBYTES;
 #pragma unroll
     for (int b = 0; b < VB; ++b) {
       const int blk = tid + b * NT, kq = blk >> 4, dq = blk & 15;
@@ -346,7 +366,8 @@ __global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p,
         uint2 w;
         w.x = uint32_t(e[0][x]) | (uint32_t(e[1][x]) << 16);
         w.y = uint32_t(e[2][x]) | (uint32_t(e[3][x]) << 16);
-        *reinterpret_cast<uint2*>(vt + (4 * dq + x) * VROW + 8 * kq) = w;
+        const int pq = (kq & ~3) | ((kq & 1) << 1) | ((kq >> 1) & 1);  // quad order 0, 2, 1, 3
+        *reinterpret_cast<uint2*>(vt + (4 * dq + x) * VROW + 8 * pq) = w;
       }
     }
   };
@@ -362,23 +383,23 @@ __global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p,
   }
   const int sw = (l32 >> 1) & 7;
 
-  auto tile = [&](int t, int buf, auto masked) {
-    const char* kb = smem + buf * (KBYTES + VBYTES);
-    const char* vt = kb + KBYTES;
+  auto tile = [&](int t, int kbuf, int vbuf, bool masked) {
+    const char* kb = smem + kbuf * KBYTES;
+    const char* vt = smem + 2 * KBYTES + vbuf * VBYTES;
     f32x16 s[QT][2];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) { s[qt][0][r] = 0.f; s[qt][1][r] = 0.f; }
+    const f32x16 zero = {};
 #pragma unroll
     for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const uint4 kf = *reinterpret_cast<const uint4*>(kb + (kt2 * 32 + l32) * 128 + ((2 * st + g) ^ sw) * 16);
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) AttnOps<bf16>::qk(s[qt][kt2], kf, qf[qt][st]);
+        for (int qt = 0; qt < QT; ++qt)  // the first k-step starts from a zero accumulator operand
+          s[qt][kt2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                               __builtin_bit_cast(bf16x8_t, qf[qt][st]),
+                                                               st == 0 ? zero : s[qt][kt2], 0, 0, 0);
       }
-    if (decltype(masked)::value) {
+    if (masked) {  // last tile only: one code path keeps O in the same registers every tile
       const int k0 = t * 64;
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt)
@@ -392,9 +413,12 @@ __global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p,
     float mnew[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      float mx = s[qt][0][0];
+      // 32 scores -> 1 with three-input maxima (v_max3_f32): 16 instructions
+      float m8[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[qt][0][r], s[qt][1][r]));
+      for (int i = 0; i < 8; ++i)
+        m8[i] = fmaxf(fmaxf(s[qt][0][2 * i], s[qt][0][2 * i + 1]), fmaxf(s[qt][1][2 * i], s[qt][1][2 * i + 1]));
+      float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
       mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
       mnew[qt] = mx > mref[qt] + 8.f ? mx : mref[qt];
       grow |= mnew[qt] != mref[qt];
@@ -429,10 +453,7 @@ __global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p,
       for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const char* vb = vrow + (kt2 * 32 + 16 * hh + 4 * g) * 2;
-          const uint2 lo = *reinterpret_cast<const uint2*>(vb);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vb + 16);
-          const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          const uint4 vf = *reinterpret_cast<const uint4*>(vrow + (kt2 * 32 + 16 * hh + 8 * g) * 2);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {
             uint4 pf;
@@ -448,23 +469,22 @@ __global__ void __launch_bounds__(WAVES * 64) attn_bf16_kernel(const AttnArgs p,
   };
 
   const int ntiles = (L + 63) / 64;
+  constexpr int AFTER_K = 4 * VB;  // loads issued after a tile's K: its V
   issue_k(0, 0);
   load_v(0);
   store_v(0);
-  wait_vm<0>();
+  wait_vm<AFTER_K>();
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) {
-      issue_k(t + 1, buf ^ 1);
-      load_v(t + 1);
-    }
-    if (t + 1 < ntiles) tile(t, buf, std::integral_constant<bool, false>{});
-    else tile(t, buf, std::integral_constant<bool, true>{});
-    if (t + 1 < ntiles) store_v(buf ^ 1);
-    wait_vm<0>();
+    // K buffer (t+1)&1 held tile t-1; the V registers held tile t, already stored
+    issue_k(t + 1, (t + 1) & 1);
+    load_v(t + 1);
+    tile(t, t & 1, t & 1, t + 1 == ntiles);
+    store_v((t + 1) & 1);
+    wait_vm<AFTER_K>();
     __syncthreads();
   }
+  wait_vm<0>();  // the zero-fill loads past the last tile land before the block's LDS is released
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
