@@ -518,9 +518,15 @@ void attention(const Exec& ex, const AttnArgs& a) {
     dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
     hipLaunchKernelGGL(attn_kernel<float>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);
   } else if (long(a.L) * a.ld * 2 < 2147483648L && a.ld % 8 == 0 && a.ldo % 4 == 0) {
-    // 4 waves x 32 queries: two sub-tiles of queries per wave (QT = 2) measured slower on
-    // gfx950 (register pressure pushes the accumulators through AGPR moves).
-    hipLaunchKernelGGL((attn_bf16_kernel<4, 1>), dim3(cdiv(a.L, 128) * a.heads * a.seqs), dim3(256), 0, ex.stream, a, c);
+    // 4 waves x 32 or 64 queries. Two query sub-tiles per wave (QT = 2) halve the K/V reads per
+    // query and win once their grid still gives each CU about two blocks (C5 global 2.46 vs
+    // 2.85 ms, C4 encoder 56 vs 62 us); below that the doubled block size leaves CUs idle
+    // (C4 global 261 vs 242 us).
+    const long blocks2 = long(cdiv(a.L, 256)) * a.heads * a.seqs;
+    if (blocks2 >= 450)
+      hipLaunchKernelGGL((attn_bf16_kernel<4, 2>), dim3(blocks2), dim3(256), 0, ex.stream, a, c);
+    else
+      hipLaunchKernelGGL((attn_bf16_kernel<4, 1>), dim3(cdiv(a.L, 128) * a.heads * a.seqs), dim3(256), 0, ex.stream, a, c);
   } else {
     dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
     hipLaunchKernelGGL(attn_kernel<bf16>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);

@@ -72,6 +72,8 @@ ATTN_CASES = [
     (6, 973, 6),
     (1, 5838, 6),
     (2, 1037, 16),
+    (6, 1037, 16),   # two query sub-tiles per wave (large grid)
+    (8, 1100, 12),   # the same with a ragged last key tile
 ]
 
 
