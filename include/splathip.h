@@ -138,11 +138,16 @@ int splat_load_mapanything_bytes(splat_ctx* ctx, const uint8_t* bytes, size_t le
 /* The reference's constants (spec NULL above). */
 void splat_ma_reference_spec(splat_ma_spec* out);
 /* MapAnything::forward(images, intrinsics), mapanything-rs/src/model.rs:86-144, for views of
- * one size. intrinsics must be NULL (the known-intrinsics ray encoder is not implemented:
- * SPLAT_BAD_ARGUMENT otherwise). */
+ * one size. intrinsics: NULL (every camera unknown) or host [V, 4] doubles fx, fy, cx, cy
+ * (pixels, pixel centres at integer coordinates) per view; a view whose fx or fy is not a
+ * finite positive number is unknown (Option::None in the reference). Known views add the ray
+ * encoder's features (ray_encoder.rs:78-86, fp32) to their patches (model.rs:97-102);
+ * SPLAT_MISSING_KEY if the checkpoint has no ray_dirs_encoder. */
 int splat_ma_forward(splat_ctx* ctx, const float* images, int V, int H, int W, const double* intrinsics,
                      splat_ma_out* out);
-int splat_ma_forward_device(splat_ctx* ctx, const float* images, int V, int H, int W, splat_ma_out* out);
+/* Same with device pointers in `images` and `out`; `intrinsics` stays a host array. */
+int splat_ma_forward_device(splat_ctx* ctx, const float* images, int V, int H, int W, const double* intrinsics,
+                            splat_ma_out* out);
 /* Dinov2::forward for every view (mapanything-rs/src/dinov2.rs:129-145): tokens [V, 1+R*C, enc_dim]. */
 int splat_ma_encode(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens);
 int splat_ma_encode_device(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens);

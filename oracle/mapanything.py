@@ -1,9 +1,10 @@
 """CPU oracle for MapAnything — TEST INFRASTRUCTURE ONLY (see oracle/common.py).
 
-Restates mapanything-rs/src/{model,dinov2,vit_block,info_sharing,dpt,heads}.rs in torch-CPU
-float32, parameterised by a spec (splathip.specs.MaSpec) so that the reference's constants
-and the benchmark's ViT-L / 768 widths both run. With enc_dim != info_dim the assumed
-`info_sharing.proj_embed` Linear maps the fused patches and raw class token to info_dim.
+Restates mapanything-rs/src/{model,dinov2,vit_block,info_sharing,dpt,heads,ray_encoder}.rs
+in torch-CPU float32, parameterised by a spec (splathip.specs.MaSpec) so that the reference's
+constants and the benchmark's ViT-L / 768 widths both run. With enc_dim != info_dim the
+assumed `info_sharing.proj_embed` Linear maps the fused patches and raw class token to
+info_dim.
 """
 from __future__ import annotations
 
@@ -20,6 +21,7 @@ RAY_MIN_NORM = 1e-8     # mapanything-rs/src/model.rs:17
 CONF_MIN = 1.0          # mapanything-rs/src/model.rs:19
 QUAT_MIN_NORM = 1e-8    # mapanything-rs/src/heads.rs:16
 MIN_SCALE = 1e-8        # mapanything-rs/src/heads.rs:17
+RAY_WIDTHS = (3 * 14 * 14, 768, 1024)  # mapanything-rs/src/ray_encoder.rs:11-12
 
 
 def encoder_forward(p, spec, images, taps=None):
@@ -136,8 +138,45 @@ def dense_output(raw, scale):
     return points, CONF_MIN + torch.exp(raw[:, 4]), raw[:, 5] > 0
 
 
-def forward(weights, spec, images, dtype=torch.float32, encoder_only=False, taps=None, info_taps=None) -> dict:
-    """mapanything-rs/src/model.rs:86-144 with no intrinsics (the `None` branch at :103)."""
+def ray_map(intrinsics, height: int, width: int) -> torch.Tensor:
+    """mapanything-rs/src/model.rs:38-54: [3, H, W] unit directions of pinhole rays, pixel
+    centres at integer coordinates, computed in f64 and stored as f32. intrinsics =
+    (fx, fy, cx, cy)."""
+    fx, fy, cx, cy = (float(v) for v in intrinsics)
+    xs = (torch.arange(width, dtype=torch.float64) - cx) / fx
+    ys = (torch.arange(height, dtype=torch.float64) - cy) / fy
+    d = torch.stack([xs[None, :].expand(height, width), ys[:, None].expand(height, width),
+                     torch.ones(height, width, dtype=torch.float64)])
+    return (d / d.norm(dim=0, keepdim=True)).float()
+
+
+def pixel_unshuffle(x: torch.Tensor, r: int) -> torch.Tensor:
+    """mapanything-rs/src/ray_encoder.rs:48-54 (torch's PixelUnshuffle): [B, C, h*r, w*r] ->
+    [B, C*r*r, h, w], channel-major, then row, then column within the block."""
+    B, Cn, H, W = x.shape
+    return x.reshape(B, Cn, H // r, r, W // r, r).permute(0, 1, 3, 5, 2, 4).reshape(B, Cn * r * r, H // r, W // r)
+
+
+def ray_encoder(p, rays: torch.Tensor) -> torch.Tensor:
+    """mapanything-rs/src/ray_encoder.rs:56-86: rays [B, 3, H, W] -> patch features [B, P, dim].
+    conv_in 3x3 (588 -> 588), two residual blocks gelu(conv2(gelu(conv1(x))) + shortcut(x))
+    (588 -> 768 -> 1024; 3x3, 3x3, 1x1), encoder.2 1x1 (1024 -> dim), LayerNorm eps 1e-6. The
+    reference runs it in f32 whatever the model dtype (model.rs:72-73)."""
+    q = "ray_dirs_encoder."
+    x = C.conv(pixel_unshuffle(rays, C.PATCH), p, q + "conv_in", padding=1)
+    for i in range(2):
+        b = f"{q}encoder.{i}."
+        h = C.gelu(C.conv(x, p, b + "conv1", padding=1))
+        x = C.gelu(C.conv(h, p, b + "conv2", padding=1) + C.conv(x, p, b + "shortcut"))
+    x = C.conv(x, p, q + "encoder.2").flatten(2).transpose(1, 2)
+    return C.layer_norm(x, p[q + "norm_layer.weight"], p[q + "norm_layer.bias"], LN_EPS)
+
+
+def forward(weights, spec, images, dtype=torch.float32, encoder_only=False, taps=None, info_taps=None,
+            intrinsics=None) -> dict:
+    """mapanything-rs/src/model.rs:86-144. intrinsics: None, or one entry per view, each None
+    (unknown camera, model.rs:103) or (fx, fy, cx, cy) (known: the ray encoder's features are
+    added to the image patches before the fusion norm, model.rs:97-102)."""
     p = C.to_torch(weights, dtype) if not isinstance(next(iter(weights.values())), torch.Tensor) else weights
     x = torch.as_tensor(np.asarray(images)).to(dtype)
     V, _, H, W = x.shape
@@ -147,7 +186,16 @@ def forward(weights, spec, images, dtype=torch.float32, encoder_only=False, taps
         tokens = encoder_forward(p, spec, x, taps)
         if encoder_only:
             return {"encoder_tokens": tokens.float()}
-        fused = C.layer_norm(tokens[:, 1:], p["fusion_norm_layer.weight"], p["fusion_norm_layer.bias"], LN_EPS)
+        patches = tokens[:, 1:]
+        if intrinsics is not None and any(k is not None for k in intrinsics):
+            rdt = torch.float64 if dtype == torch.float64 else torch.float32
+            rp = {k: v.to(rdt) for k, v in p.items() if k.startswith("ray_dirs_encoder.")}
+            add = torch.zeros_like(patches)
+            for v, k in enumerate(intrinsics):
+                if k is not None:
+                    add[v] = ray_encoder(rp, ray_map(k, H, W)[None].to(rdt))[0].to(patches.dtype)
+            patches = patches + add
+        fused = C.layer_norm(patches, p["fusion_norm_layer.weight"], p["fusion_norm_layer.bias"], LN_EPS)
         classes = tokens[:, :1]
         info_patches, info_classes = fused, classes
         if spec.has_proj:

@@ -61,14 +61,42 @@ void da3_device(Context* ctx, const float* images, int V, int H, int W, const sp
   ctx->run(key, use_graphs(ctx), [&] { ctx->da3->forward(images, V, H, W, out, ref, ctx->hooks); });
 }
 
+// Known cameras: host [V, 4] (fx, fy, cx, cy) -> device [V, 5] with a known flag (fx and fy
+// finite and > 0; other views keep the unknown-camera path, model.rs:103). NULL when no view
+// is known. Copied before the (possibly graph-replayed) forward, which reads it from device
+// memory.
+const double* stage_cameras(Context* ctx, const double* intrinsics, int V) {
+  if (!intrinsics) return nullptr;
+  std::vector<double> cam(size_t(V) * 5, 0.0);
+  bool any = false;
+  for (int v = 0; v < V; ++v) {
+    const double* k = intrinsics + 4 * v;
+    const bool known = std::isfinite(k[0]) && std::isfinite(k[1]) && std::isfinite(k[2]) && std::isfinite(k[3]) &&
+                       k[0] > 0 && k[1] > 0;
+    if (known) {
+      for (int j = 0; j < 4; ++j) cam[size_t(v) * 5 + j] = k[j];
+      cam[size_t(v) * 5 + 4] = 1.0;
+      any = true;
+    } else {
+      cam[size_t(v) * 5 + 0] = cam[size_t(v) * 5 + 1] = 1.0;  // finite placeholders, never added
+    }
+  }
+  if (!any) return nullptr;
+  double* d = static_cast<double*>(staging(ctx, 18, cam.size() * sizeof(double)));
+  SPLAT_HIP(hipMemcpyAsync(d, cam.data(), cam.size() * sizeof(double), hipMemcpyHostToDevice, ctx->stream));
+  SPLAT_HIP(hipStreamSynchronize(ctx->stream));
+  return d;
+}
+
 void ma_device(Context* ctx, const float* images, int V, int H, int W, const splat_ma_out& out, float* tokens,
-               bool encoder_only) {
+               bool encoder_only, const double* intrinsics = nullptr) {
   SPLAT_CHECK(ctx->ma != nullptr, NOT_LOADED, "no MapAnything model loaded");
   check_images(images, V, H, W);
   ctx->ma->prepare(V, H, W);
-  Context::GraphKey key{encoder_only ? 2 : 1, V, H, W, images,
-                        {out.raw, out.quaternion, out.translation, out.scale, out.points, out.conf, out.mask, tokens}};
-  ctx->run(key, use_graphs(ctx), [&] { ctx->ma->forward(images, V, H, W, out, tokens, encoder_only, ctx->hooks); });
+  const double* cam = encoder_only ? nullptr : stage_cameras(ctx, intrinsics, V);
+  Context::GraphKey key{encoder_only ? 2 : (cam ? 3 : 1), V, H, W, images,
+                        {out.raw, out.quaternion, out.translation, out.scale, out.points, out.conf, out.mask, tokens, cam}};
+  ctx->run(key, use_graphs(ctx), [&] { ctx->ma->forward(images, V, H, W, out, tokens, encoder_only, ctx->hooks, cam); });
 }
 
 void load_ma(Context* ctx, SafeTensors& st, const splat_ma_spec* spec, int dtype) {
@@ -241,10 +269,11 @@ int splat_load_mapanything_bytes(splat_ctx* ctx, const uint8_t* bytes, size_t le
   });
 }
 
-int splat_ma_forward_device(splat_ctx* ctx, const float* images, int V, int H, int W, splat_ma_out* out) {
+int splat_ma_forward_device(splat_ctx* ctx, const float* images, int V, int H, int W, const double* intrinsics,
+                            splat_ma_out* out) {
   return guard(C(ctx), [&] {
     SPLAT_CHECK(out != nullptr, BAD_ARGUMENT, "out is NULL");
-    ma_device(C(ctx), images, V, H, W, *out, nullptr, false);
+    ma_device(C(ctx), images, V, H, W, *out, nullptr, false, intrinsics);
   });
 }
 
@@ -253,7 +282,6 @@ int splat_ma_forward(splat_ctx* ctx, const float* images, int V, int H, int W, c
   Context* c = C(ctx);
   return guard(c, [&] {
     SPLAT_CHECK(out != nullptr, BAD_ARGUMENT, "out is NULL");
-    SPLAT_CHECK(intrinsics == nullptr, BAD_ARGUMENT, "known intrinsics (the ray encoder) are not supported");
     check_images(images, V, H, W);
     SPLAT_CHECK(c->ma != nullptr, NOT_LOADED, "no MapAnything model loaded");
     const size_t hw = size_t(H) * W, img = size_t(V) * 3 * hw;
@@ -267,7 +295,7 @@ int splat_ma_forward(splat_ctx* ctx, const float* images, int V, int H, int W, c
     dev.conf = out->conf ? static_cast<float*>(staging(c, 16, V * hw * 4)) : nullptr;
     dev.mask = out->mask ? static_cast<uint8_t*>(staging(c, 17, V * hw)) : nullptr;
     SPLAT_HIP(hipMemcpyAsync(d_img, images, img * 4, hipMemcpyHostToDevice, c->stream));
-    ma_device(c, d_img, V, H, W, dev, nullptr, false);
+    ma_device(c, d_img, V, H, W, dev, nullptr, false, intrinsics);
     d2h(c, out->raw, dev.raw, V * 6 * hw);
     d2h(c, out->quaternion, dev.quaternion, V * 4);
     d2h(c, out->translation, dev.translation, V * 3);

@@ -107,7 +107,7 @@ __device__ inline void store8(const GemmArgs& p, const float* v, long idx) {
 }
 
 // Epilogue of 8 consecutive columns n..n+7 of row m: bias, activation, table add, LayerScale,
-// residuals, store. `vec`: all of them exist and every operand is 16-byte aligned for them.
+// residuals, post-residual activation, store. `vec`: all of them exist and every operand is 16-byte aligned for them.
 template <typename T>
 __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool vec) {
   const long row = p.rm_P ? (m / p.rm_P) * p.rm_n + p.rm_off + m % p.rm_P : m;
@@ -121,6 +121,8 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
     if (p.gamma) { load8(p.gamma, n, true, t); for (int k = 0; k < 8; ++k) v[k] *= t[k]; }
     if (p.res) { load8(p.res, row * p.ldres + n, rf, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
     if (p.res2) { load8(p.res2, row * p.ldres2 + n, rf2, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    if (p.act_post == ACT_GELU) for (int k = 0; k < 8; ++k) v[k] = gelu_erf(v[k]);
+    else if (p.act_post == ACT_RELU) for (int k = 0; k < 8; ++k) v[k] = fmaxf(v[k], 0.f);
     store8<T>(p, v, out_index(p, m, n, row));
     return;
   }
@@ -134,6 +136,8 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
     if (p.gamma) x *= p.gamma[nn];
     if (p.res) x += load_res<T>(p.res, row * p.ldres + nn, p.res_f32);
     if (p.res2) x += load_res<T>(p.res2, row * p.ldres2 + nn, p.res2_f32);
+    if (p.act_post == ACT_GELU) x = gelu_erf(x);
+    else if (p.act_post == ACT_RELU) x = fmaxf(x, 0.f);
     const long idx = out_index(p, m, nn, row);
     if (p.out_f32) reinterpret_cast<float*>(p.out)[idx] = x;
     else reinterpret_cast<T*>(p.out)[idx] = from_f<T>(x);
@@ -259,7 +263,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
 
 // Which epilogue variant a launch needs (host side; `a.epi_vec` already set).
 inline int epi_kind(const GemmArgs& a) {
-  if (!a.epi_vec || a.rm_P || a.store != STORE_ROWS || a.addtab || a.res2) return EPI_FULL;
+  if (!a.epi_vec || a.rm_P || a.store != STORE_ROWS || a.addtab || a.res2 || a.act_post) return EPI_FULL;
   return (a.res || a.gamma) ? EPI_RES : EPI_BIAS;
 }
 

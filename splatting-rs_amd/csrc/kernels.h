@@ -38,6 +38,7 @@ struct GemmArgs {
   const float* gamma = nullptr;
   const void* res = nullptr; long ldres = 0; int res_f32 = 0;
   const void* res2 = nullptr; long ldres2 = 0; int res2_f32 = 0;
+  int act_post = ACT_NONE;  // activation applied after the residual adds
   void* out = nullptr; long ldc = 0; int out_f32 = 0;
   int rm_P = 0, rm_n = 0, rm_off = 0;
   int store = STORE_ROWS;
@@ -107,6 +108,13 @@ void set_camera_tokens(const Exec& ex, float* xs, int V, int n, int dim, const f
 // and when cam_out != null: cam_out[v] = cat(within[v*n], xs[v*n]) (fp32, no norm).
 void da3_hook(const Exec& ex, int dt, const float* within, const float* xs, int V, int n, int dim,
               const float* bnw, const float* bnb, const float* hnw, const float* hnb, void* out, float* cam_out);
+
+// Known-camera rays (mapanything-rs/src/model.rs:38-54) already pixel-unshuffled by 14
+// (ray_encoder.rs:48-54): out [V, H/14, W/14, 588] fp32, channel c*196 + 14*i + j for ray
+// component c of pixel (14*row + i, 14*col + j). cam [V, 5] f64 device: fx, fy, cx, cy, known.
+void ray_unshuffled(const Exec& ex, const double* cam, int V, int H, int W, float* out);
+// xs[v*n + 1 + p, :] += feat[v*P + p, :] for the views whose cam[v, 4] != 0.
+void add_view_features(const Exec& ex, float* xs, int V, int n, int P, int dim, const float* feat, const double* cam);
 
 // Generic elementwise helpers.
 void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count);

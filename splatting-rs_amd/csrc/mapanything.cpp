@@ -1,6 +1,7 @@
 // MapAnything: weights (mapanything-rs/src/{model.rs:69-81, dinov2.rs:90-101,
-// info_sharing.rs:39-47, dpt.rs:147-182,254-273, heads.rs:55-121}) and the forward of
-// MapAnything::forward (model.rs:86-144) with no intrinsics, all views batched.
+// info_sharing.rs:39-47, dpt.rs:147-182,254-273, heads.rs:55-121, ray_encoder.rs:56-76}) and
+// the forward of MapAnything::forward (model.rs:86-144), all views batched; views with known
+// intrinsics add the ray encoder's features to their patches (model.rs:97-102).
 #include <algorithm>
 #include <cstring>
 
@@ -74,6 +75,22 @@ MaModel::MaModel(Context& ctx, const SafeTensors& st, const splat_ma_spec& spec,
   scale_mlp_[0] = L.linear("scale_head.mlp.0.0", sd, sd);
   scale_mlp_[1] = L.linear("scale_head.mlp.1.0", sd, sd);
   scale_out_ = L.linear("scale_head.output_proj", 1, sd);
+  // The reference always builds the ray encoder (model.rs:73); a checkpoint without it still
+  // serves unknown cameras here, and a forward with known ones reports the missing keys.
+  has_rays_ = st.has("ray_dirs_encoder.conv_in.weight");
+  if (has_rays_) {
+    Loader LR(ctx, st, F32, "ray_dirs_encoder.");
+    const int w[3] = {3 * PATCH * PATCH, 768, 1024};
+    ray_in_ = LR.conv("conv_in", w[0], w[0], 3);
+    for (int i = 0; i < 2; ++i) {
+      const std::string b = "encoder." + std::to_string(i);
+      ray_c1_[i] = LR.conv(b + ".conv1", w[i + 1], w[i], 3);
+      ray_c2_[i] = LR.conv(b + ".conv2", w[i + 1], w[i + 1], 3);
+      ray_sc_[i] = LR.conv(b + ".shortcut", w[i + 1], w[i], 1);
+    }
+    ray_out_ = LR.conv("encoder.2", e, w[2], 1);
+    ray_norm_ = LR.ln("norm_layer", e);
+  }
 }
 
 void MaModel::prepare(int V, int H, int W) {
@@ -88,7 +105,7 @@ void MaModel::prepare(int V, int H, int W) {
 }
 
 void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_out& out, float* enc_tokens,
-                      bool encoder_only, const Hooks& hooks) {
+                      bool encoder_only, const Hooks& hooks, const double* cam) {
   const Exec& ex = ctx_.ex;
   Arena& ar = ctx_.arena;
   const int R = H / PATCH, C = W / PATCH, P = R * C, n = P + 1;
@@ -138,6 +155,42 @@ void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_o
     ar.release(m);
   }
   if (encoder_only) return;
+
+  // ---- known cameras (model.rs:97-102): ray features added to the image patches, in fp32
+  // (ray_encoder.rs:78-86: pixel-unshuffle, conv_in, two residual blocks
+  // gelu(conv2(gelu(conv1(x))) + shortcut(x)), 1x1 to enc_dim, LayerNorm). Every view is
+  // encoded; the add skips the views whose camera is unknown.
+  if (cam) {
+    SPLAT_CHECK(has_rays_, MISSING_KEY, "ray_dirs_encoder.* (known intrinsics need the ray encoder)");
+    const size_t m = ar.mark();
+    const long rows = long(V) * P;
+    float* rays = ar.alloc_t<float>(size_t(rows) * 588);
+    ray_unshuffled(ex, cam, V, H, W, rays);
+    float* x = ar.alloc_t<float>(size_t(rows) * 588);
+    gemm(ex, conv_args(ray_in_, F32, rays, V, R, C, 1, x));
+    for (int i = 0; i < 2; ++i) {
+      const int co = ray_c1_[i].cout;
+      float* h = ar.alloc_t<float>(size_t(rows) * co);
+      GemmArgs g1 = conv_args(ray_c1_[i], F32, x, V, R, C, 1, h);
+      g1.act = ACT_GELU;
+      gemm(ex, g1);
+      float* sc = ar.alloc_t<float>(size_t(rows) * co);
+      gemm(ex, conv_args(ray_sc_[i], F32, x, V, R, C, 1, sc));
+      float* y = ar.alloc_t<float>(size_t(rows) * co);
+      GemmArgs g2 = conv_args(ray_c2_[i], F32, h, V, R, C, 1, y);
+      g2.res = sc;
+      g2.ldres = co;
+      g2.act_post = ACT_GELU;
+      gemm(ex, g2);
+      x = y;
+    }
+    float* f = ar.alloc_t<float>(size_t(rows) * e);
+    gemm(ex, conv_args(ray_out_, F32, x, V, R, C, 1, f));
+    float* fn = ar.alloc_t<float>(size_t(rows) * e);
+    layer_norm(ex, F32, f, e, F32, fn, e, rows, e, ray_norm_.w, ray_norm_.b, LN_EPS);
+    add_view_features(ex, xe, V, n, P, e, fn, cam);
+    ar.release(m);
+  }
 
   // ---- fusion norm on the patches (model.rs:106); the class token stays raw (model.rs:108)
   void* hook0 = ar.alloc(size_t(V) * P * e * es);

@@ -715,6 +715,48 @@ void add_rows(const Exec& ex, float* xs, int rows, int dim, const float* vec) {
   SPLAT_HIP(hipGetLastError());
 }
 
+// One thread per pixel: the unit direction ((x - cx)/fx, (y - cy)/fy, 1)/norm in f64
+// (mapanything-rs/src/model.rs:42-50), stored as f32 at its pixel-unshuffled position.
+__global__ void ray_unshuffled_kernel(const double* cam, int V, int H, int W, float* out) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long hw = (long)H * W;
+  if (id >= (long)V * hw) return;
+  const int v = int(id / hw), pix = int(id - v * hw), y = pix / W, x = pix - y * W;
+  const double* c = cam + v * 5;
+  const double dx = (double(x) - c[2]) / c[0], dy = (double(y) - c[3]) / c[1];
+  const double inv = 1.0 / sqrt(dx * dx + dy * dy + 1.0);
+  const int R = H / 14, C = W / 14, r = y / 14, i = y - r * 14, col = x / 14, j = x - col * 14;
+  float* o = out + ((long(v) * R + r) * C + col) * 588 + i * 14 + j;
+  o[0] = float(dx * inv);
+  o[196] = float(dy * inv);
+  o[392] = float(inv);
+}
+
+void ray_unshuffled(const Exec& ex, const double* cam, int V, int H, int W, float* out) {
+  if (ex.dry || V == 0) return;
+  SPLAT_CHECK(H % 14 == 0 && W % 14 == 0, BAD_SHAPE, "ray map: H and W must be multiples of 14");
+  ProfScope ps(ex, "ray_map", 0.0, double(V) * H * W * 12);
+  hipLaunchKernelGGL(ray_unshuffled_kernel, dim3(cdiv((long)V * H * W, 256)), dim3(256), 0, ex.stream, cam, V, H, W,
+                     out);
+  SPLAT_HIP(hipGetLastError());
+}
+
+__global__ void add_view_features_kernel(float* xs, int V, int n, int P, int dim, const float* feat,
+                                         const double* cam) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)V * P * dim) return;
+  const long row = id / dim;
+  const int v = int(row / P), p = int(row - long(v) * P), c = int(id - row * dim);
+  if (cam[v * 5 + 4] != 0.0) xs[(long(v) * n + 1 + p) * dim + c] += feat[id];
+}
+
+void add_view_features(const Exec& ex, float* xs, int V, int n, int P, int dim, const float* feat, const double* cam) {
+  if (ex.dry || V == 0) return;
+  hipLaunchKernelGGL(add_view_features_kernel, dim3(cdiv((long)V * P * dim, 256)), dim3(256), 0, ex.stream, xs, V, n,
+                     P, dim, feat, cam);
+  SPLAT_HIP(hipGetLastError());
+}
+
 __global__ void copy_rows_kernel(float* dst, long lddst, const float* src, long ldsrc, int rows, int dim) {
   const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= (long)rows * dim) return;

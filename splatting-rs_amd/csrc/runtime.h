@@ -206,10 +206,12 @@ class Da3Model {
 class MaModel {
  public:
   MaModel(Context& ctx, const SafeTensors& st, const splat_ma_spec& spec, int dt);
+  // cam: NULL (no view has a known camera) or device f64 [V, 5] = fx, fy, cx, cy, known.
   void forward(const float* images, int V, int H, int W, const splat_ma_out& out, float* enc_tokens, bool encoder_only,
-               const Hooks& hooks);
+               const Hooks& hooks, const double* cam = nullptr);
   void prepare(int V, int H, int W);
   const splat_ma_spec& spec() const { return spec_; }
+  bool has_ray_encoder() const { return has_rays_; }
   int dt() const { return dt_; }
 
  private:
@@ -239,6 +241,10 @@ class MaModel {
   Lin pose_res_[2][3];
   Lin pose_mlp_[2], pose_t_, pose_rot_;
   Lin scale_proj_, scale_mlp_[2], scale_out_;
+  // known-camera ray encoder (ray_encoder.rs:56-76), fp32 whatever the model dtype
+  bool has_rays_ = false;
+  Conv ray_in_, ray_c1_[2], ray_c2_[2], ray_sc_[2], ray_out_;
+  LN ray_norm_;
   std::map<std::tuple<int, int>, Tables> tables_;
 };
 

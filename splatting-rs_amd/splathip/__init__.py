@@ -84,7 +84,8 @@ SIGNATURES = {
     "splat_load_mapanything_bytes": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(MaSpecC), C.c_int]),
     "splat_ma_reference_spec": (None, [C.POINTER(MaSpecC)]),
     "splat_ma_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.POINTER(MaOutC)]),
-    "splat_ma_forward_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(MaOutC)]),
+    "splat_ma_forward_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                          C.POINTER(MaOutC)]),
     "splat_ma_encode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "splat_ma_encode_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "splat_kernel_gemm": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int,
@@ -218,7 +219,18 @@ class Context:
                                                     DTYPES[dtype]))
         self.ma_spec = spec or specs.MA_SPECS["reference"]
 
-    def ma_forward(self, images: np.ndarray, raw: bool = True, dense: bool = True) -> dict:
+    @staticmethod
+    def _cameras(intrinsics, V: int):
+        """None, or one entry per view: None (unknown camera) or (fx, fy, cx, cy)."""
+        if intrinsics is None:
+            return None
+        assert len(intrinsics) == V, "one intrinsics entry per view"
+        k = np.zeros((V, 4), np.float64)
+        for v, e in enumerate(intrinsics):
+            k[v] = e if e is not None else (np.nan, np.nan, np.nan, np.nan)
+        return k
+
+    def ma_forward(self, images: np.ndarray, raw: bool = True, dense: bool = True, intrinsics=None) -> dict:
         x = np.ascontiguousarray(images, np.float32)
         V, _, H, W = x.shape
         out = {
@@ -231,13 +243,17 @@ class Context:
             "mask": np.empty((V, H, W), np.uint8) if dense else None,
         }
         o = MaOutC(*[_ptr(out[k]) for k in ("raw", "quaternion", "translation", "scale", "points", "conf", "mask")])
-        self.check(self._lib.splat_ma_forward(self.handle, _ptr(x), V, H, W, None, C.byref(o)))
+        k = self._cameras(intrinsics, V)
+        self.check(self._lib.splat_ma_forward(self.handle, _ptr(x), V, H, W, _ptr(k) if k is not None else None,
+                                              C.byref(o)))
         return out
 
-    def ma_forward_device(self, images_ptr: int, V: int, H: int, W: int, outs: dict):
+    def ma_forward_device(self, images_ptr: int, V: int, H: int, W: int, outs: dict, intrinsics=None):
         o = MaOutC(*[C.c_void_p(outs.get(k) or 0) for k in
                      ("raw", "quaternion", "translation", "scale", "points", "conf", "mask")])
-        self.check(self._lib.splat_ma_forward_device(self.handle, C.c_void_p(images_ptr), V, H, W, C.byref(o)))
+        k = self._cameras(intrinsics, V)
+        self.check(self._lib.splat_ma_forward_device(self.handle, C.c_void_p(images_ptr), V, H, W,
+                                                     _ptr(k) if k is not None else None, C.byref(o)))
 
     def ma_encode(self, images: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(images, np.float32)

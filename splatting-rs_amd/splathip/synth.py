@@ -169,6 +169,15 @@ def ma_shapes(spec: MaSpec) -> Shapes:
     _linear(out, "scale_head.mlp.0.0", sd, sd)
     _linear(out, "scale_head.mlp.1.0", sd, sd)
     _linear(out, "scale_head.output_proj", 1, sd)
+    # known-intrinsics ray encoder, mapanything-rs/src/ray_encoder.rs:56-76 (fixed widths)
+    w0, w1, w2 = 3 * PATCH * PATCH, 768, 1024
+    _conv(out, "ray_dirs_encoder.conv_in", w0, w0, 3)
+    for i, (ci, co) in enumerate(((w0, w1), (w1, w2))):
+        _conv(out, f"ray_dirs_encoder.encoder.{i}.conv1", co, ci, 3)
+        _conv(out, f"ray_dirs_encoder.encoder.{i}.conv2", co, co, 3)
+        _conv(out, f"ray_dirs_encoder.encoder.{i}.shortcut", co, ci, 1)
+    _conv(out, "ray_dirs_encoder.encoder.2", e, w2, 1)
+    _ln(out, "ray_dirs_encoder.norm_layer", e)
     return out
 
 

@@ -82,8 +82,12 @@ def test_checkpoint_key_maps():
     assert ma["dense_head.0.input_process.0.0.0.weight"][0] == (96, 1024, 1, 1)
     assert ma["dense_head.0.input_process.1.0.0.weight"][0] == (192, 768, 1, 1)
     assert "dense_head.0.input_process.2.0.1.weight" not in ma
+    assert ma["ray_dirs_encoder.conv_in.weight"][0] == (588, 588, 3, 3)
+    assert ma["ray_dirs_encoder.encoder.1.conv2.weight"][0] == (1024, 1024, 3, 3)
+    assert ma["ray_dirs_encoder.encoder.2.weight"][0] == (1024, 1024, 1, 1)
     n = sum(int(np.prod(s)) for s, _ in ma.values())
-    assert 480e6 < n < 520e6
+    nray = sum(int(np.prod(s)) for k, (s, _) in ma.items() if k.startswith("ray_dirs_encoder."))
+    assert 480e6 < n - nray < 520e6 and 31e6 < nray < 32e6
 
 
 def test_configs_match_the_benchmark_table():

@@ -125,3 +125,62 @@ def test_ma_errors(ctx, ma_weights):
     with pytest.raises(splathip.SplatError) as e:
         ctx.load_mapanything(path, bad, "f32")
     assert e.value.code in (splathip.MISSING_KEY, splathip.SHAPE_MISMATCH)
+
+
+# --- known cameras: the ray encoder (mapanything-rs/src/model.rs:97-102, ray_encoder.rs) -----
+
+CAMS = [(60.0, 62.0, 34.5, 27.5), (48.0, 48.0, 30.0, 20.0), (90.0, 70.0, 10.0, 40.0)]
+
+
+@pytest.mark.parametrize("known", [(0, 1, 2), (1,)])
+def test_ma_known_cameras_fp32(ctx, ma_weights, known):
+    path, w, spec = ma_weights[("tiny_proj", 1.0)]
+    images = synth.procedural_images(3, 56, 70, seed=8)
+    intr = [CAMS[v] if v in known else None for v in range(3)]
+    report("ma.rays.fp32", known=known)
+    ctx.load_mapanything(path, spec, "f32")
+    out = ctx.ma_forward(images, intrinsics=intr)
+    ref = O.forward(w, spec, images, intrinsics=intr)
+    _check_fp32(out, ref)
+    # the cameras change the result (the ray features are not lost on the way)
+    plain = O.forward(w, spec, images)
+    assert rel_err(ref["raw"].numpy(), plain["raw"].numpy()) > 1e-3
+
+
+def test_ma_known_cameras_bf16_and_graph_replay(ctx, ma_weights):
+    path, w, spec = ma_weights[("tiny", 1.0)]
+    images = synth.procedural_images(3, 42, 56, seed=9)
+    intr = [CAMS[0], None, CAMS[2]]
+    ctx.load_mapanything(path, spec, "bf16")
+    ref = O.forward(w, spec, images, intrinsics=intr)
+    ctx.set_graphs(True)
+    try:
+        outs = [ctx.ma_forward(images, intrinsics=intr) for _ in range(3)]
+        other = ctx.ma_forward(images, intrinsics=[CAMS[1], None, CAMS[0]])
+        again = ctx.ma_forward(images, intrinsics=intr)
+    finally:
+        ctx.set_graphs(False)
+    for o in outs + [again]:
+        c = cosine(o["raw"], ref["raw"].numpy())
+        report("ma.rays.bf16", cos_raw=f"{c:.6f}")
+        assert c >= 0.999
+        assert np.array_equal(o["raw"], outs[0]["raw"])
+    # new camera values on the same captured graph are read at replay
+    ref_other = O.forward(w, spec, images, intrinsics=[CAMS[1], None, CAMS[0]])
+    assert cosine(other["raw"], ref_other["raw"].numpy()) >= 0.999
+    assert not np.array_equal(other["raw"], outs[0]["raw"])
+
+
+def test_ma_known_cameras_need_the_ray_encoder(ctx, ma_weights, weights_dir):
+    path, w, spec = ma_weights[("tiny", 1e-5)]
+    stripped = {k: v for k, v in w.items() if not k.startswith("ray_dirs_encoder.")}
+    p2 = os.path.join(str(weights_dir), "ma_tiny_norays.safetensors")
+    synth.save(p2, stripped)
+    ctx.load_mapanything(p2, spec, "f32")
+    images = synth.procedural_images(2, 28, 42, seed=1)
+    a = ctx.ma_forward(images)                       # unknown cameras need no ray encoder
+    b = ctx.ma_forward(images, intrinsics=[None, None])
+    assert np.array_equal(a["raw"], b["raw"])
+    with pytest.raises(splathip.SplatError) as e:
+        ctx.ma_forward(images, intrinsics=[CAMS[0], None])
+    assert e.value.code == splathip.MISSING_KEY

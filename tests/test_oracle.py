@@ -243,3 +243,70 @@ def test_da3_outputs_are_positive_and_rays_finite():
     assert torch.all(out["depth"] > 0) and torch.all(out["depth_conf"] > 1)
     assert torch.isfinite(out["ray_logits"]).all() and out["ray_logits"].shape == (3, 7, 16, 24)
     assert out["pose_encoding"].shape == (3, 9) and torch.all(out["pose_encoding"][:, 7:] >= 0)
+
+
+# --- known-camera ray encoder (mapanything-rs/src/{model.rs:38-54, ray_encoder.rs}) -----------
+
+def test_pixel_unshuffle_orders_channel_then_row_then_column():
+    # KAT of mapanything-rs/src/ray_encoder.rs:93-103: one channel, 2x4 image, factor 2
+    x = torch.arange(8.0).reshape(1, 1, 2, 4)
+    out = OM.pixel_unshuffle(x, 2)[0]
+    assert out.tolist() == [[[0.0, 2.0]], [[1.0, 3.0]], [[4.0, 6.0]], [[5.0, 7.0]]]
+    # and torch's PixelUnshuffle (the routine the reference names) at the encoder's factor
+    y = torch.randn(2, 3, 28, 42)
+    assert torch.equal(OM.pixel_unshuffle(y, 14), F.pixel_unshuffle(y, 14))
+
+
+def test_ray_map_is_a_unit_pinhole_direction():
+    fx, fy, cx, cy = 300.0, 250.0, 20.5, 10.0
+    r = OM.ray_map((fx, fy, cx, cy), 28, 42).double()
+    assert r.shape == (3, 28, 42)
+    assert float((r.norm(dim=0) - 1).abs().max()) < 1e-6
+    # pixel (x=41, y=0): direction ((41 - cx)/fx, (0 - cy)/fy, 1) normalised
+    d = np.array([(41 - cx) / fx, (0 - cy) / fy, 1.0])
+    assert np.allclose(r[:, 0, 41].numpy(), d / np.linalg.norm(d), atol=1e-7)
+    # the z component is the cosine to the optical axis: largest near the principal point
+    assert int(r[2].argmax()) == 10 * 42 + 20
+
+
+def test_ray_encoder_shortcut_path_closed_form():
+    # With conv_in the identity, conv1/conv2 zero and identity shortcuts, each residual block
+    # is gelu(0 + x) = gelu(x) (ray_encoder.rs:38-42: the activation follows the add), so the
+    # encoder reduces to LN(W @ gelu(gelu(unshuffle(rays)))) with zero-padded channels.
+    g = torch.Generator().manual_seed(1)
+    e = 64
+    w0, w1, w2 = OM.RAY_WIDTHS
+    q = "ray_dirs_encoder."
+    p = {}
+    cin = torch.zeros(w0, w0, 3, 3)
+    cin[:, :, 1, 1] = torch.eye(w0)
+    p[q + "conv_in.weight"], p[q + "conv_in.bias"] = cin, torch.zeros(w0)
+    for i, (a, b) in enumerate(((w0, w1), (w1, w2))):
+        k = f"{q}encoder.{i}."
+        p[k + "conv1.weight"], p[k + "conv1.bias"] = torch.zeros(b, a, 3, 3), torch.zeros(b)
+        p[k + "conv2.weight"], p[k + "conv2.bias"] = torch.zeros(b, b, 3, 3), torch.zeros(b)
+        sc = torch.zeros(b, a, 1, 1)
+        sc[:a, :, 0, 0] = torch.eye(a)
+        p[k + "shortcut.weight"], p[k + "shortcut.bias"] = sc, torch.zeros(b)
+    W = torch.randn(e, w2, generator=g) * 0.05
+    p[q + "encoder.2.weight"], p[q + "encoder.2.bias"] = W[:, :, None, None], torch.zeros(e)
+    lw, lb = 1 + 0.1 * torch.randn(e, generator=g), 0.1 * torch.randn(e, generator=g)
+    p[q + "norm_layer.weight"], p[q + "norm_layer.bias"] = lw, lb
+    rays = OM.ray_map((60.0, 70.0, 21.0, 13.0), 28, 42)[None]
+    got = OM.ray_encoder(p, rays)[0]
+    u = OM.pixel_unshuffle(rays, 14)[0].reshape(w0, -1).T          # [P, 588]
+    z = torch.zeros(u.shape[0], w2)
+    z[:, :w0] = F.gelu(F.gelu(u))
+    want = F.layer_norm(z @ W.T, (e,), lw, lb, 1e-6)
+    assert torch.allclose(got, want, atol=1e-5)
+
+
+def test_mapanything_unknown_cameras_match_no_intrinsics():
+    spec = specs.MA_SPECS["tiny"]
+    w = synth.generate(synth.ma_shapes(spec), seed=3)
+    images = synth.procedural_images(2, 28, 42, seed=2)
+    a = OM.forward(w, spec, images)
+    b = OM.forward(w, spec, images, intrinsics=[None, None])
+    c = OM.forward(w, spec, images, intrinsics=[(50.0, 50.0, 21.0, 14.0), None])
+    assert torch.equal(a["raw"], b["raw"])
+    assert not torch.equal(a["raw"], c["raw"])
