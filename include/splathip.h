@@ -97,6 +97,21 @@ typedef struct splat_ma_out {
   uint8_t* mask;         /* [V, H, W] unambiguous (raw mask logit > 0) (optional)          */
 } splat_ma_out;
 
+/* Outputs of the post-forward reconstructions: one point map and camera per view, all in view
+ * 0's camera frame (OpenCV axes), as depthanything3-rs/src/pipeline.rs:17-42 (Camera,
+ * ReconstructedView) and mapanything-rs/src/reconstruction.rs:8-19. Caller-owned host
+ * buffers; NULL skips an optional field. */
+typedef struct splat_recon_out {
+  float* points;            /* [V, H, W, 3] scene points (required)                          */
+  float* conf;              /* [V, H, W] confidence after multi-view cleaning (required)     */
+  float* depth;             /* [V, H, W] camera-frame depth (optional)                       */
+  double* rotation;         /* [V, 3, 3] camera to scene, row-major (optional)               */
+  double* translation;      /* [V, 3] (optional)                                             */
+  double* focal;            /* [V, 2] fx, fy in pixels (optional)                            */
+  double* principal_point;  /* [V, 2] cx, cy (optional)                                      */
+  int32_t reference_view;   /* DA3: the network's reference view; MapAnything: 0             */
+} splat_recon_out;
+
 /* --- context ------------------------------------------------------------------------------ */
 
 /* Replaces candle's `Device::new_metal(0)` / `Device::Cpu` choice (depthanything3-rs/src/main.rs:136). */
@@ -129,6 +144,15 @@ int splat_da3_forward_raw(splat_ctx* ctx, const float* images, int V, int H, int
 int splat_da3_forward_raw_device(splat_ctx* ctx, const float* images, int V, int H, int W, splat_da3_out* out,
                                  int32_t* ref_view_device);
 
+/* depthanything3-rs/src/pipeline.rs:52-133 (reconstruct): forward, per-view camera from the pose
+ * encoding, poses relative to view 0, depth unprojected through each view's intrinsics, then
+ * mapanything-rs/src/cleaning.rs:28-64 (zero the confidence of points in front of another
+ * view's more confident foreground). Geometry runs on the device. foreground: [V, H, W]
+ * (non-zero = foreground; NULL = every pixel, the reference's opaque images). Returns
+ * SPLAT_NONFINITE (outputs written) where DepthAnything3::forward asserts (model.rs:139-146). */
+int splat_da3_reconstruct(splat_ctx* ctx, const float* images, int V, int H, int W, const uint8_t* foreground,
+                          splat_recon_out* out);
+
 /* --- MapAnything ----------------------------------------------------------------------------- */
 
 /* MapAnything::new(VarBuilder over the checkpoint), mapanything-rs/src/model.rs:69-81;
@@ -148,6 +172,12 @@ int splat_ma_forward(splat_ctx* ctx, const float* images, int V, int H, int W, c
 /* Same with device pointers in `images` and `out`; `intrinsics` stays a host array. */
 int splat_ma_forward_device(splat_ctx* ctx, const float* images, int V, int H, int W, const double* intrinsics,
                             splat_ma_out* out);
+/* mapanything-rs/src/pipeline.rs:41-104 (reconstruct): forward (intrinsics as splat_ma_forward),
+ * poses relative to view 0, fit_intrinsics on the camera-frame points (pipeline.rs:18-39),
+ * ambiguous pixels' confidence zeroed, then the multi-view cleaning; focal = (fx, fy) of the
+ * fit (the reference's Camera keeps their mean). Geometry runs on the device. */
+int splat_ma_reconstruct(splat_ctx* ctx, const float* images, int V, int H, int W, const double* intrinsics,
+                         const uint8_t* foreground, splat_recon_out* out);
 /* Dinov2::forward for every view (mapanything-rs/src/dinov2.rs:129-145): tokens [V, 1+R*C, enc_dim]. */
 int splat_ma_encode(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens);
 int splat_ma_encode_device(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens);

@@ -53,6 +53,17 @@ int splat_profile_end(splat_ctx* ctx, splat_kernel_stat* stats, int max, int* co
 int splat_kernel_resize_bilinear(splat_ctx* ctx, int dtype, const void* in, int V, int Hi, int Wi, int C, void* out,
                                  int Ho, int Wo);
 
+/* The device geometry of splat_da3_reconstruct / splat_ma_reconstruct on given network outputs
+ * (all device pointers, fp32 unless noted): DA3 mode when depth != NULL (depth [V,H,W],
+ * pose_encoding [V,9]); MapAnything mode otherwise (points_in_camera [V,H,W,3], quaternion
+ * [V,4] xyzw, translation [V,3], mask [V,H,W] u8 unambiguous). conf [V,H,W]; foreground
+ * [V,H,W] u8 or NULL. Out: cameras [V,16] f64 (R row-major, t, fx, fy, cx, cy, view 0's
+ * frame), points [V,H,W,3], conf_out [V,H,W]. */
+int splat_kernel_reconstruct(splat_ctx* ctx, int V, int H, int W, const float* depth, const float* pose_encoding,
+                             const float* points_in_camera, const float* quaternion, const float* translation,
+                             const float* conf, const uint8_t* mask, const uint8_t* foreground, double* cameras,
+                             float* points, float* conf_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -452,6 +452,132 @@ int splat_kernel_resize_bilinear(splat_ctx* ctx, int dtype, const void* in, int 
   });
 }
 
+int splat_kernel_reconstruct(splat_ctx* ctx, int V, int H, int W, const float* depth, const float* pose_encoding,
+                             const float* points_in_camera, const float* quaternion, const float* translation,
+                             const float* conf, const uint8_t* mask, const uint8_t* foreground, double* cameras,
+                             float* points, float* conf_out) {
+  Context* c = C(ctx);
+  return guard(c, [&] {
+    SPLAT_CHECK(V > 0 && H > 0 && W > 0 && conf && cameras && points && conf_out, BAD_ARGUMENT, "geometry args");
+    const size_t px = size_t(V) * H * W;
+    float* d_conf0 = static_cast<float*>(staging(c, 21, px * 4));
+    double* d_fit = depth ? nullptr : static_cast<double*>(staging(c, 24, size_t(V) * 4 * 8));
+    reconstruct_geometry(c->ex, V, H, W, depth, pose_encoding, points_in_camera, quaternion, translation, conf, mask,
+                         foreground, cameras, d_fit, d_conf0, points, conf_out);
+  });
+}
+
+// --- post-forward reconstruction ---------------------------------------------------------------
+
+namespace {
+
+void recon_outputs(Context* c, int V, int H, int W, const double* d_cam, const float* d_points, const float* d_conf,
+                   const float* d_depth, int depth_stride, splat_recon_out* out) {
+  const size_t px = size_t(V) * H * W;
+  d2h(c, out->points, d_points, px * 3);
+  d2h(c, out->conf, d_conf, px);
+  std::vector<double> cam(size_t(V) * 16);
+  SPLAT_HIP(hipMemcpyAsync(cam.data(), d_cam, cam.size() * 8, hipMemcpyDeviceToHost, c->stream));
+  std::vector<float> dep;
+  if (out->depth) {
+    dep.resize((px - 1) * depth_stride + 1);  // the z of the last point ends the buffer
+    SPLAT_HIP(hipMemcpyAsync(dep.data(), d_depth, dep.size() * 4, hipMemcpyDeviceToHost, c->stream));
+  }
+  SPLAT_HIP(hipStreamSynchronize(c->stream));
+  for (int v = 0; v < V; ++v) {
+    const double* k = cam.data() + size_t(v) * 16;
+    if (out->rotation) std::memcpy(out->rotation + size_t(v) * 9, k, 9 * 8);
+    if (out->translation) std::memcpy(out->translation + size_t(v) * 3, k + 9, 3 * 8);
+    if (out->focal) std::memcpy(out->focal + size_t(v) * 2, k + 12, 2 * 8);
+    if (out->principal_point) std::memcpy(out->principal_point + size_t(v) * 2, k + 14, 2 * 8);
+  }
+  if (out->depth)
+    for (size_t i = 0; i < px; ++i) out->depth[i] = dep[i * depth_stride];
+}
+
+const uint8_t* stage_foreground(Context* c, const uint8_t* fg, size_t px) {
+  if (!fg) return nullptr;
+  uint8_t* d = static_cast<uint8_t*>(staging(c, 25, px));
+  SPLAT_HIP(hipMemcpyAsync(d, fg, px, hipMemcpyHostToDevice, c->stream));
+  return d;
+}
+
+}  // namespace
+
+int splat_da3_reconstruct(splat_ctx* ctx, const float* images, int V, int H, int W, const uint8_t* foreground,
+                          splat_recon_out* out) {
+  Context* c = C(ctx);
+  bool finite = true;
+  int rc = guard(c, [&] {
+    SPLAT_CHECK(out != nullptr && out->points && out->conf, BAD_ARGUMENT, "points and conf are required");
+    check_images(images, V, H, W);
+    SPLAT_CHECK(c->da3 != nullptr, NOT_LOADED, "no Depth Anything 3 model loaded");
+    const size_t hw = size_t(H) * W, px = size_t(V) * hw;
+    float* d_img = static_cast<float*>(staging(c, 0, size_t(V) * 3 * hw * 4));
+    splat_da3_out dev{};
+    dev.depth = static_cast<float*>(staging(c, 1, px * 4));
+    dev.depth_conf = static_cast<float*>(staging(c, 2, px * 4));
+    dev.pose_encoding = static_cast<float*>(staging(c, 4, V * 9 * 4));
+    int32_t* d_ref = static_cast<int32_t*>(staging(c, 6, 4));
+    double* d_cam = static_cast<double*>(staging(c, 20, size_t(V) * 16 * 8));
+    float* d_conf0 = static_cast<float*>(staging(c, 21, px * 4));
+    float* d_points = static_cast<float*>(staging(c, 22, px * 12));
+    float* d_conf = static_cast<float*>(staging(c, 23, px * 4));
+    SPLAT_HIP(hipMemcpyAsync(d_img, images, px * 3 * 4, hipMemcpyHostToDevice, c->stream));
+    const uint8_t* d_fg = stage_foreground(c, foreground, px);
+    da3_device(c, d_img, V, H, W, dev, d_ref);
+    reconstruct_geometry(c->ex, V, H, W, dev.depth, dev.pose_encoding, nullptr, nullptr, nullptr, dev.depth_conf,
+                         nullptr, d_fg, d_cam, nullptr, d_conf0, d_points, d_conf);
+    int32_t ref = 0;
+    SPLAT_HIP(hipMemcpyAsync(&ref, d_ref, 4, hipMemcpyDeviceToHost, c->stream));
+    std::vector<float> pose(size_t(V) * 9), depth(px);
+    SPLAT_HIP(hipMemcpyAsync(pose.data(), dev.pose_encoding, pose.size() * 4, hipMemcpyDeviceToHost, c->stream));
+    SPLAT_HIP(hipMemcpyAsync(depth.data(), dev.depth, px * 4, hipMemcpyDeviceToHost, c->stream));
+    recon_outputs(c, V, H, W, d_cam, d_points, d_conf, dev.depth, 1, out);
+    out->reference_view = ref;
+    // DepthAnything3::forward's asserts (model.rs:139-146): finite positive depth, finite camera
+    for (float d : depth) finite = finite && std::isfinite(d) && d > 0.f;
+    for (float e : pose) finite = finite && std::isfinite(e);
+  });
+  if (rc != OK) return rc;
+  if (!finite) {
+    c->last_error = "depth or camera is not finite and positive (outputs written)";
+    return NONFINITE;
+  }
+  return OK;
+}
+
+int splat_ma_reconstruct(splat_ctx* ctx, const float* images, int V, int H, int W, const double* intrinsics,
+                         const uint8_t* foreground, splat_recon_out* out) {
+  Context* c = C(ctx);
+  return guard(c, [&] {
+    SPLAT_CHECK(out != nullptr && out->points && out->conf, BAD_ARGUMENT, "points and conf are required");
+    check_images(images, V, H, W);
+    SPLAT_CHECK(c->ma != nullptr, NOT_LOADED, "no MapAnything model loaded");
+    const size_t hw = size_t(H) * W, px = size_t(V) * hw;
+    float* d_img = static_cast<float*>(staging(c, 10, size_t(V) * 3 * hw * 4));
+    splat_ma_out dev{};
+    dev.quaternion = static_cast<float*>(staging(c, 12, V * 4 * 4));
+    dev.translation = static_cast<float*>(staging(c, 13, V * 3 * 4));
+    dev.scale = static_cast<float*>(staging(c, 14, 4));
+    dev.points = static_cast<float*>(staging(c, 15, px * 12));
+    dev.conf = static_cast<float*>(staging(c, 16, px * 4));
+    dev.mask = static_cast<uint8_t*>(staging(c, 17, px));
+    double* d_cam = static_cast<double*>(staging(c, 20, size_t(V) * 16 * 8));
+    float* d_conf0 = static_cast<float*>(staging(c, 21, px * 4));
+    float* d_points = static_cast<float*>(staging(c, 22, px * 12));
+    float* d_conf = static_cast<float*>(staging(c, 23, px * 4));
+    double* d_fit = static_cast<double*>(staging(c, 24, size_t(V) * 4 * 8));
+    SPLAT_HIP(hipMemcpyAsync(d_img, images, px * 3 * 4, hipMemcpyHostToDevice, c->stream));
+    const uint8_t* d_fg = stage_foreground(c, foreground, px);
+    ma_device(c, d_img, V, H, W, dev, nullptr, false, intrinsics);
+    reconstruct_geometry(c->ex, V, H, W, nullptr, nullptr, dev.points, dev.quaternion, dev.translation, dev.conf,
+                         dev.mask, d_fg, d_cam, d_fit, d_conf0, d_points, d_conf);
+    recon_outputs(c, V, H, W, d_cam, d_points, d_conf, dev.points + 2, 3, out);
+    out->reference_view = 0;
+  });
+}
+
 int splat_ma_encode(splat_ctx* ctx, const float* images, int V, int H, int W, float* tokens) {
   Context* c = C(ctx);
   return guard(c, [&] {

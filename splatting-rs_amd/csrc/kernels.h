@@ -116,6 +116,17 @@ void ray_unshuffled(const Exec& ex, const double* cam, int V, int H, int W, floa
 // xs[v*n + 1 + p, :] += feat[v*P + p, :] for the views whose cam[v, 4] != 0.
 void add_view_features(const Exec& ex, float* xs, int V, int n, int P, int dim, const float* feat, const double* cam);
 
+// Post-forward geometry, all on the device (depthanything3-rs/src/pipeline.rs:44-133,
+// mapanything-rs/src/pipeline.rs:18-104, cleaning.rs:28-64). DA3: depth [V,H,W] and
+// pose_enc [V,9]; MapAnything (depth NULL): camera-frame points pts_cam [V,H,W,3], xyzw quat
+// [V,4], metric trans [V,3], unambiguous mask, fitted [V,4] scratch. conf [V,H,W] in;
+// fg [V,H,W] foreground (NULL = all). Out: cam [V,16] (R row-major, t, fx, fy, cx, cy in
+// view 0's frame), conf0 scratch, points [V,H,W,3] in view 0's frame, cleaned conf_out.
+void reconstruct_geometry(const Exec& ex, int V, int H, int W, const float* depth, const float* pose_enc,
+                          const float* pts_cam, const float* quat, const float* trans, const float* conf,
+                          const uint8_t* mask, const uint8_t* fg, double* cam, double* fitted, float* conf0,
+                          float* points, float* conf_out);
+
 // Generic elementwise helpers.
 void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count);
 void add_rows(const Exec& ex, float* xs, int rows, int dim, const float* vec);           // xs[r] += vec

@@ -846,4 +846,165 @@ void scale_rows(const Exec& ex, const float* x, int rows, int dim, const float* 
   SPLAT_HIP(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------------------
+// Post-forward geometry (depthanything3-rs/src/pipeline.rs:44-133, mapanything-rs/src/
+// {pipeline.rs:18-104, reconstruction.rs:22-33, cleaning.rs:28-64}), in f64 like the
+// reference's nalgebra code. cam [V, 16] f64 per view: camera -> view-0 frame rotation R
+// (row-major), translation t, focal (fx, fy), principal point (cx, cy).
+
+__device__ inline void quat_rotation(double x, double y, double z, double w, double* R) {
+  const double n = sqrt(x * x + y * y + z * z + w * w);  // UnitQuaternion::from_quaternion normalises
+  x /= n; y /= n; z /= n; w /= n;
+  R[0] = 1 - 2 * (y * y + z * z); R[1] = 2 * (x * y - z * w);     R[2] = 2 * (x * z + y * w);
+  R[3] = 2 * (x * y + z * w);     R[4] = 1 - 2 * (x * x + z * z); R[5] = 2 * (y * z - x * w);
+  R[6] = 2 * (x * z - y * w);     R[7] = 2 * (y * z + x * w);     R[8] = 1 - 2 * (x * x + y * y);
+}
+
+// One thread per view. DA3 (pose_enc != NULL): t, xyzw quaternion, fov_h, fov_w
+// (camera_head.rs:28-53); MapAnything: quaternion, metric translation and the fitted
+// intrinsics (fitted [V, 4] = cx, cy, fx, fy). Poses are re-expressed relative to view 0
+// (reconstruction.rs:22-33): R0^T R, R0^T (t - t0).
+__global__ void recon_cameras_kernel(int V, int H, int W, const float* pose_enc, const float* quat, const float* trans,
+                                     const double* fitted, double* cam) {
+  const int v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= V) return;
+  double R[9], R0[9], t[3], t0[3];
+  auto pose = [&](int u, double* Ru, double* tu) {
+    if (pose_enc) {
+      const float* e = pose_enc + u * 9;
+      quat_rotation(e[3], e[4], e[5], e[6], Ru);
+      for (int k = 0; k < 3; ++k) tu[k] = e[k];
+    } else {
+      const float* q = quat + u * 4;
+      quat_rotation(q[0], q[1], q[2], q[3], Ru);
+      for (int k = 0; k < 3; ++k) tu[k] = trans[u * 3 + k];
+    }
+  };
+  pose(v, R, t);
+  pose(0, R0, t0);
+  double* c = cam + v * 16;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) c[i * 3 + j] = R0[0 * 3 + i] * R[0 * 3 + j] + R0[1 * 3 + i] * R[1 * 3 + j] + R0[2 * 3 + i] * R[2 * 3 + j];
+  for (int i = 0; i < 3; ++i)
+    c[9 + i] = R0[0 * 3 + i] * (t[0] - t0[0]) + R0[1 * 3 + i] * (t[1] - t0[1]) + R0[2 * 3 + i] * (t[2] - t0[2]);
+  if (pose_enc) {
+    const double fov_h = pose_enc[v * 9 + 7], fov_w = pose_enc[v * 9 + 8];
+    c[12] = W / 2.0 / fmax(tan(fov_w / 2.0), 1e-6);
+    c[13] = H / 2.0 / fmax(tan(fov_h / 2.0), 1e-6);
+    c[14] = W / 2.0;
+    c[15] = H / 2.0;
+  } else {
+    c[12] = fitted[v * 4 + 2];
+    c[13] = fitted[v * 4 + 3];
+    c[14] = fitted[v * 4 + 0];
+    c[15] = fitted[v * 4 + 1];
+  }
+}
+
+// One block per view: least squares pixel = centre + focal * coordinate / z per axis over
+// every (side/50)-th pixel (mapanything-rs/src/pipeline.rs:18-39); out [V, 4] = cx, cy, fx, fy.
+__global__ void __launch_bounds__(256) fit_intrinsics_kernel(const float* pts, int H, int W, double* out) {
+  const int v = blockIdx.x;
+  const int sy = max(H / 50, 1), sx = max(W / 50, 1);
+  const int ny = (H + sy - 1) / sy, nx = (W + sx - 1) / sx;
+  double acc[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};  // per axis: n, sum r, sum r^2, sum pix, sum r*pix
+  for (int s = threadIdx.x; s < ny * nx; s += 256) {
+    const int y = (s / nx) * sy, x = (s % nx) * sx;
+    const float* p = pts + ((long(v) * H + y) * W + x) * 3;
+    const double z = p[2];
+    const double rx = double(p[0]) / z, ry = double(p[1]) / z;
+    acc[0] += 1; acc[1] += rx; acc[2] += rx * rx; acc[3] += x; acc[4] += rx * x;
+    acc[5] += 1; acc[6] += ry; acc[7] += ry * ry; acc[8] += y; acc[9] += ry * y;
+  }
+  __shared__ double red[10][256];
+  for (int k = 0; k < 10; ++k) red[k][threadIdx.x] = acc[k];
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w)
+      for (int k = 0; k < 10; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x < 2) {
+    const int a = threadIdx.x * 5;
+    const double n = red[a][0], sr = red[a + 1][0], srr = red[a + 2][0], sp = red[a + 3][0], srp = red[a + 4][0];
+    const double det = n * srr - sr * sr;
+    out[v * 4 + threadIdx.x] = (sp * srr - sr * srp) / det;      // centre
+    out[v * 4 + 2 + threadIdx.x] = (n * srp - sr * sp) / det;    // focal
+  }
+}
+
+// One thread per pixel: camera-frame point (DA3: unprojected depth, pipeline.rs:44-51;
+// MapAnything: the network's point) -> view-0 frame, R p + t, stored f32. conf0 = the
+// confidence before cleaning (MapAnything: 0 where the mask calls the pixel ambiguous).
+__global__ void unproject_kernel(int V, int H, int W, const float* depth, const float* pts_cam, const float* conf,
+                                 const uint8_t* mask, const double* cam, float* points, float* conf0) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long hw = (long)H * W;
+  if (id >= V * hw) return;
+  const int v = int(id / hw), pix = int(id - v * hw), y = pix / W, x = pix - y * W;
+  const double* c = cam + v * 16;
+  double p[3];
+  if (depth) {
+    const double d = depth[id];
+    p[0] = (x - c[14]) / c[12] * d;
+    p[1] = (y - c[15]) / c[13] * d;
+    p[2] = d;
+  } else {
+    for (int k = 0; k < 3; ++k) p[k] = pts_cam[id * 3 + k];
+  }
+  for (int i = 0; i < 3; ++i) points[id * 3 + i] = float(c[i * 3] * p[0] + c[i * 3 + 1] * p[1] + c[i * 3 + 2] * p[2] + c[9 + i]);
+  conf0[id] = mask && !mask[id] ? 0.f : conf[id];
+}
+
+// One thread per pixel of image i: zero its confidence if, seen from another view j, it lies
+// in front (by more than 2%) of j's foreground depth at the pixel it projects to and is less
+// confident (cleaning.rs:28-64). Projections use the view's mean focal; pixels round half
+// away from zero (f64::round). Reads conf0 only, so every comparison sees the originals.
+__global__ void clean_kernel(int V, int H, int W, const float* points, const float* conf0, const float* depth,
+                             int dstride, const uint8_t* fg, const double* cam, float* conf) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long hw = (long)H * W;
+  if (id >= V * hw) return;
+  const int i = int(id / hw);
+  const float ci = conf0[id];
+  bool zero = false;
+  if (!fg || fg[id]) {
+    const double px = points[id * 3], py = points[id * 3 + 1], pz = points[id * 3 + 2];
+    for (int j = 0; j < V && !zero; ++j) {
+      if (j == i) continue;
+      const double* c = cam + j * 16;
+      const double dx = px - c[9], dy = py - c[10], dz = pz - c[11];
+      const double qx = c[0] * dx + c[3] * dy + c[6] * dz;   // R^T (p - t)
+      const double qy = c[1] * dx + c[4] * dy + c[7] * dz;
+      const double qz = c[2] * dx + c[5] * dy + c[8] * dz;
+      if (!(qz > 0.0)) continue;
+      const double f = (c[12] + c[13]) / 2.0;
+      const double u = round(f * qx / qz + c[14]), vv = round(f * qy / qz + c[15]);
+      if (!(u >= 0.0 && vv >= 0.0 && u < double(W) && vv < double(H))) continue;
+      const long op = long(j) * hw + long(vv) * W + long(u);
+      if ((!fg || fg[op]) && qz < (1.0 - 0.02) * double(depth[op * dstride]) && ci < conf0[op]) zero = true;
+    }
+  }
+  conf[id] = zero ? 0.f : ci;
+}
+
+void reconstruct_geometry(const Exec& ex, int V, int H, int W, const float* depth, const float* pose_enc,
+                          const float* pts_cam, const float* quat, const float* trans, const float* conf,
+                          const uint8_t* mask, const uint8_t* fg, double* cam, double* fitted, float* conf0,
+                          float* points, float* conf_out) {
+  if (ex.dry || V == 0) return;
+  const bool da3 = depth != nullptr;
+  SPLAT_CHECK(da3 ? pose_enc != nullptr : (pts_cam && quat && trans && fitted), BAD_ARGUMENT, "geometry inputs");
+  const long px = long(V) * H * W;
+  ProfScope ps(ex, "geometry", 0.0, double(px) * (da3 ? 4 : 12) * 2 + double(px) * 4 * (V + 2) + double(px) * 12);
+  if (!da3) hipLaunchKernelGGL(fit_intrinsics_kernel, dim3(V), dim3(256), 0, ex.stream, pts_cam, H, W, fitted);
+  hipLaunchKernelGGL(recon_cameras_kernel, dim3(cdiv(V, 64)), dim3(64), 0, ex.stream, V, H, W, pose_enc, quat, trans,
+                     fitted, cam);
+  hipLaunchKernelGGL(unproject_kernel, dim3(cdiv(px, 256)), dim3(256), 0, ex.stream, V, H, W, depth, pts_cam, conf,
+                     mask, cam, points, conf0);
+  hipLaunchKernelGGL(clean_kernel, dim3(cdiv(px, 256)), dim3(256), 0, ex.stream, V, H, W, points, conf0,
+                     da3 ? depth : pts_cam + 2, da3 ? 1 : 3, fg, cam, conf_out);
+  SPLAT_HIP(hipGetLastError());
+}
+
 }  // namespace splat

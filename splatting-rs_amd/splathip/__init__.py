@@ -57,6 +57,12 @@ class MaOutC(C.Structure):
                 ("points", C.c_void_p), ("conf", C.c_void_p), ("mask", C.c_void_p)]
 
 
+class ReconOutC(C.Structure):
+    _fields_ = [("points", C.c_void_p), ("conf", C.c_void_p), ("depth", C.c_void_p), ("rotation", C.c_void_p),
+                ("translation", C.c_void_p), ("focal", C.c_void_p), ("principal_point", C.c_void_p),
+                ("reference_view", C.c_int32)]
+
+
 class KernelStatC(C.Structure):
     _fields_ = [("name", C.c_char * 32), ("launches", C.c_int), ("ms", C.c_double), ("flops", C.c_double),
                 ("bytes", C.c_double)]
@@ -87,6 +93,10 @@ SIGNATURES = {
     "splat_ma_forward_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                           C.POINTER(MaOutC)]),
     "splat_ma_encode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "splat_da3_reconstruct": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                        C.POINTER(ReconOutC)]),
+    "splat_ma_reconstruct": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                       C.POINTER(ReconOutC)]),
     "splat_ma_encode_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "splat_kernel_gemm": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int,
                                     C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
@@ -100,6 +110,7 @@ SIGNATURES = {
                                                 C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "splat_kernel_resize_bilinear": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
                                                C.c_void_p, C.c_int, C.c_int]),
+    "splat_kernel_reconstruct": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int] + [C.c_void_p] * 11),
 }
 
 _lib = None
@@ -255,6 +266,38 @@ class Context:
         self.check(self._lib.splat_ma_forward_device(self.handle, C.c_void_p(images_ptr), V, H, W,
                                                      _ptr(k) if k is not None else None, C.byref(o)))
 
+    @staticmethod
+    def _recon_out(V: int, H: int, W: int):
+        out = {"points": np.empty((V, H, W, 3), np.float32), "conf": np.empty((V, H, W), np.float32),
+               "depth": np.empty((V, H, W), np.float32), "rotation": np.empty((V, 3, 3), np.float64),
+               "translation": np.empty((V, 3), np.float64), "focal": np.empty((V, 2), np.float64),
+               "principal_point": np.empty((V, 2), np.float64)}
+        o = ReconOutC(*[_ptr(out[k]) for k in ("points", "conf", "depth", "rotation", "translation", "focal",
+                                                "principal_point")], 0)
+        return out, o
+
+    def da3_reconstruct(self, images: np.ndarray, foreground=None) -> dict:
+        """depthanything3-rs/src/pipeline.rs:52-133 with the geometry on the device."""
+        x = np.ascontiguousarray(images, np.float32)
+        V, _, H, W = x.shape
+        out, o = self._recon_out(V, H, W)
+        fg = None if foreground is None else np.ascontiguousarray(foreground, np.uint8)
+        self.check(self._lib.splat_da3_reconstruct(self.handle, _ptr(x), V, H, W, _ptr(fg) if fg is not None else None,
+                                                   C.byref(o)))
+        out["reference_view"] = int(o.reference_view)
+        return out
+
+    def ma_reconstruct(self, images: np.ndarray, intrinsics=None, foreground=None) -> dict:
+        """mapanything-rs/src/pipeline.rs:41-104 with the geometry on the device."""
+        x = np.ascontiguousarray(images, np.float32)
+        V, _, H, W = x.shape
+        out, o = self._recon_out(V, H, W)
+        k = self._cameras(intrinsics, V)
+        fg = None if foreground is None else np.ascontiguousarray(foreground, np.uint8)
+        self.check(self._lib.splat_ma_reconstruct(self.handle, _ptr(x), V, H, W, _ptr(k) if k is not None else None,
+                                                  _ptr(fg) if fg is not None else None, C.byref(o)))
+        return out
+
     def ma_encode(self, images: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(images, np.float32)
         V, _, H, W = x.shape
@@ -300,6 +343,12 @@ class Context:
     def kernel_resize_bilinear(self, dtype, inp, V, Hi, Wi, Cc, out, Ho, Wo):
         self.check(self._lib.splat_kernel_resize_bilinear(self.handle, dtype, C.c_void_p(inp), V, Hi, Wi, Cc,
                                                           C.c_void_p(out), Ho, Wo))
+
+    def kernel_reconstruct(self, V, H, W, depth=0, pose_encoding=0, points_in_camera=0, quaternion=0, translation=0,
+                           conf=0, mask=0, foreground=0, cameras=0, points=0, conf_out=0):
+        ptrs = [depth, pose_encoding, points_in_camera, quaternion, translation, conf, mask, foreground, cameras,
+                points, conf_out]
+        self.check(self._lib.splat_kernel_reconstruct(self.handle, V, H, W, *[C.c_void_p(x or 0) for x in ptrs]))
 
 
 def reference_ma_spec() -> dict:

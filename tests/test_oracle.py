@@ -310,3 +310,60 @@ def test_mapanything_unknown_cameras_match_no_intrinsics():
     c = OM.forward(w, spec, images, intrinsics=[(50.0, 50.0, 21.0, 14.0), None])
     assert torch.equal(a["raw"], b["raw"])
     assert not torch.equal(a["raw"], c["raw"])
+
+
+# --- post-forward geometry (oracle/geometry.py) ----------------------------------------------
+
+from oracle import geometry as OG
+
+
+def test_cleaning_zeroes_the_less_confident_point_in_front():
+    # KAT of mapanything-rs/src/cleaning.rs:83-103: two cameras at the origin looking down z;
+    # image 0 sees a point at depth 1 (conf 2), image 1 one at depth 2 behind it (conf 3).
+    points = np.array([[[[0, 0, 1.0]]], [[[0, 0, 2.0]]]], np.float32)
+    conf = np.array([[[2.0]], [[3.0]]], np.float32)
+    depths = np.array([[[1.0]], [[2.0]]], np.float32)
+    cams = [{"R": np.eye(3), "t": np.zeros(3), "focal": 1.0, "pp": np.zeros(2)}] * 2
+    out = OG.clean(points, conf, depths, np.ones((2, 1, 1), bool), cams)
+    assert out[0, 0, 0] == 0.0 and out[1, 0, 0] == 3.0
+    # background points are never zeroed, and equal confidence keeps both
+    assert OG.clean(points, conf, depths, np.array([[[False]], [[True]]]), cams)[0, 0, 0] == 2.0
+    assert OG.clean(points, np.full_like(conf, 3.0), depths, np.ones((2, 1, 1), bool), cams)[0, 0, 0] == 3.0
+
+
+def test_relative_to_first_is_identity_for_the_first_view():
+    rng = np.random.default_rng(0)
+    poses = []
+    for _ in range(3):
+        q = rng.normal(size=4)
+        poses.append((OD.quaternion_to_rotation(*q), rng.normal(size=3)))
+    rel = OG.relative_to_first(poses)
+    assert np.allclose(rel[0][0], np.eye(3)) and np.allclose(rel[0][1], 0)
+    R0, t0 = poses[0]
+    for (R, t), (Rr, tr) in zip(poses, rel):           # composing with the first pose undoes it
+        assert np.allclose(R0 @ Rr, R) and np.allclose(R0 @ tr + t0, t)
+
+
+def test_fit_intrinsics_recovers_a_pinhole_camera():
+    rng = np.random.default_rng(1)
+    H, W, fx, fy, cx, cy = 60, 110, 91.5, 88.0, 52.25, 31.5
+    xs, ys = np.meshgrid(np.arange(W, dtype=np.float64), np.arange(H, dtype=np.float64))
+    z = rng.uniform(0.5, 4.0, size=(H, W))
+    pts = np.stack([(xs - cx) / fx * z, (ys - cy) / fy * z, z], -1).astype(np.float32)
+    centre, focal = OG.fit_intrinsics(pts)
+    assert np.allclose(centre, [cx, cy], atol=1e-3) and np.allclose(focal, [fx, fy], rtol=1e-5)
+
+
+def test_unprojection_projects_back_to_its_pixel():
+    rng = np.random.default_rng(2)
+    depth = rng.uniform(0.5, 3.0, size=(7, 9))
+    f, pp = np.array([5.0, 6.0]), np.array([4.5, 3.5])
+    p = OG.unproject(depth, f, pp)
+    u = f[0] * p[..., 0] / p[..., 2] + pp[0]
+    v = f[1] * p[..., 1] / p[..., 2] + pp[1]
+    xs, ys = np.meshgrid(np.arange(9), np.arange(7))
+    assert np.allclose(u, xs) and np.allclose(v, ys) and np.allclose(p[..., 2], depth)
+
+
+def test_f64_round_goes_away_from_zero():
+    assert OG._round(np.array([2.5, -2.5, 0.4, -0.4, 1.5]).astype(np.float64)).tolist() == [3.0, -3.0, 0.0, -0.0, 2.0]
