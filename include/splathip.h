@@ -128,6 +128,12 @@ int splat_set_graphs(splat_ctx* ctx, int enable);
 /* Per-block residual taps (NULL to disable); replaces nothing in the reference: a test hook. */
 int splat_set_debug_taps(splat_ctx* ctx, splat_tap_fn fn, void* user);
 
+/* mapanything-rs/src/image_input.rs:195-216 (to_model_input, used by both crates' preprocess):
+ * host RGBA u8 [V, H, W, 4] (already resized and cropped) -> device images [V, 3, H, W] f32,
+ * ImageNet-normalised, and device foreground [V, H, W] u8 = alpha >= 128 (NULL: skipped).
+ * Uploads 4 bytes per pixel instead of 12; enqueued on splat_stream. */
+int splat_to_model_input(splat_ctx* ctx, const uint8_t* rgba, int V, int H, int W, float* images, uint8_t* foreground);
+
 /* --- Depth Anything 3 ------------------------------------------------------------------------ */
 
 /* weights::load_model(variant, strategy, Some(path), dtype, device), depthanything3-rs/src/weights.rs:26-48

@@ -216,3 +216,19 @@ def vit_block(x, p, name, swiglu: bool, block_eps: float, qk_norm: bool = False,
 
 def to_torch(weights: dict, dtype=torch.float32) -> dict:
     return {k: torch.as_tensor(np.asarray(v)).to(dtype) for k, v in weights.items()}
+
+
+IMAGENET_MEAN = np.array([0.485, 0.456, 0.406], np.float32)   # mapanything-rs/src/image_input.rs:113
+IMAGENET_STD = np.array([0.229, 0.224, 0.225], np.float32)    # mapanything-rs/src/image_input.rs:114
+FOREGROUND_MIN_ALPHA = 128                                      # mapanything-rs/src/image_input.rs:22
+
+
+def to_model_input(rgba: np.ndarray):
+    """mapanything-rs/src/image_input.rs:195-216 for [V, H, W, 4] u8: f32 images [V, 3, H, W] =
+    ((x * (1/255) + 0) - mean) / std in f32, in candle's op order (affine, broadcast_sub,
+    broadcast_div), and foreground = alpha >= 128."""
+    x = np.asarray(rgba, np.uint8)
+    rgb = x[..., :3].astype(np.float32).transpose(0, 3, 1, 2)
+    v = rgb * np.float32(1.0 / 255.0) + np.float32(0.0)
+    v = (v - IMAGENET_MEAN[None, :, None, None]) / IMAGENET_STD[None, :, None, None]
+    return v.astype(np.float32), x[..., 3] >= FOREGROUND_MIN_ALPHA

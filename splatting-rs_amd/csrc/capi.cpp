@@ -467,6 +467,18 @@ int splat_kernel_reconstruct(splat_ctx* ctx, int V, int H, int W, const float* d
   });
 }
 
+int splat_to_model_input(splat_ctx* ctx, const uint8_t* rgba, int V, int H, int W, float* images,
+                         uint8_t* foreground) {
+  Context* c = C(ctx);
+  return guard(c, [&] {
+    SPLAT_CHECK(rgba && images && V > 0 && H > 0 && W > 0, BAD_ARGUMENT, "to_model_input args");
+    const size_t px = size_t(V) * H * W;
+    uint8_t* d = static_cast<uint8_t*>(staging(c, 26, px * 4));
+    SPLAT_HIP(hipMemcpyAsync(d, rgba, px * 4, hipMemcpyHostToDevice, c->stream));
+    to_model_input(c->ex, d, V, H, W, images, foreground);
+  });
+}
+
 // --- post-forward reconstruction ---------------------------------------------------------------
 
 namespace {

@@ -127,6 +127,9 @@ void reconstruct_geometry(const Exec& ex, int V, int H, int W, const float* dept
                           const uint8_t* mask, const uint8_t* fg, double* cam, double* fitted, float* conf0,
                           float* points, float* conf_out);
 
+// RGBA u8 [V,H,W,4] -> normalised images [V,3,H,W] f32 and foreground [V,H,W] (NULL: skipped).
+void to_model_input(const Exec& ex, const uint8_t* rgba, int V, int H, int W, float* img, uint8_t* fg);
+
 // Generic elementwise helpers.
 void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count);
 void add_rows(const Exec& ex, float* xs, int rows, int dim, const float* vec);           // xs[r] += vec

@@ -1007,4 +1007,27 @@ void reconstruct_geometry(const Exec& ex, int V, int H, int W, const float* dept
   SPLAT_HIP(hipGetLastError());
 }
 
+// mapanything-rs/src/image_input.rs:195-216 (to_model_input) for V images of one size:
+// RGBA u8 [V, H, W, 4] -> ImageNet-normalised [V, 3, H, W] f32 ((x * (1/255) - mean) / std,
+// candle's affine then broadcast ops, in that order) and foreground = alpha >= 128
+// (FOREGROUND_MIN_ALPHA, image_input.rs:22).
+__global__ void to_model_input_kernel(const uint8_t* rgba, int V, long hw, float* img, uint8_t* fg) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= V * hw) return;
+  const long v = id / hw, p = id - v * hw;
+  const uchar4 px = reinterpret_cast<const uchar4*>(rgba)[id];
+  const float mean[3] = {0.485f, 0.456f, 0.406f}, stdv[3] = {0.229f, 0.224f, 0.225f};
+  const float scale = float(1.0 / 255.0);
+  const float c[3] = {float(px.x), float(px.y), float(px.z)};
+  for (int k = 0; k < 3; ++k) img[(v * 3 + k) * hw + p] = (c[k] * scale + 0.0f - mean[k]) / stdv[k];
+  if (fg) fg[id] = px.w >= 128 ? 1 : 0;
+}
+
+void to_model_input(const Exec& ex, const uint8_t* rgba, int V, int H, int W, float* img, uint8_t* fg) {
+  if (ex.dry || V == 0) return;
+  const long hw = long(H) * W;
+  hipLaunchKernelGGL(to_model_input_kernel, dim3(cdiv(V * hw, 256)), dim3(256), 0, ex.stream, rgba, V, hw, img, fg);
+  SPLAT_HIP(hipGetLastError());
+}
+
 }  // namespace splat

@@ -93,6 +93,7 @@ SIGNATURES = {
     "splat_ma_forward_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                           C.POINTER(MaOutC)]),
     "splat_ma_encode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "splat_to_model_input": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "splat_da3_reconstruct": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                         C.POINTER(ReconOutC)]),
     "splat_ma_reconstruct": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
@@ -275,6 +276,13 @@ class Context:
         o = ReconOutC(*[_ptr(out[k]) for k in ("points", "conf", "depth", "rotation", "translation", "focal",
                                                 "principal_point")], 0)
         return out, o
+
+    def to_model_input_device(self, rgba: np.ndarray, images_ptr: int, foreground_ptr: int = 0):
+        """RGBA u8 [V, H, W, 4] (host) -> normalised images and foreground in device memory."""
+        x = np.ascontiguousarray(rgba, np.uint8)
+        V, H, W, _ = x.shape
+        self.check(self._lib.splat_to_model_input(self.handle, _ptr(x), V, H, W, C.c_void_p(images_ptr),
+                                                  C.c_void_p(foreground_ptr or 0)))
 
     def da3_reconstruct(self, images: np.ndarray, foreground=None) -> dict:
         """depthanything3-rs/src/pipeline.rs:52-133 with the geometry on the device."""

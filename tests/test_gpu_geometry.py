@@ -165,3 +165,18 @@ def test_geometry_kernel_ma_cleaning(ctx):
     assert np.allclose(got["focal"], K[:, :2], rtol=1e-4) and np.allclose(got["principal_point"], K[:, 2:], atol=1e-3)
     zeroed = float(np.mean(ref["conf"] == 0))
     assert np.mean(mask == 0) + 0.05 < zeroed < 0.9, zeroed   # ambiguous pixels plus cleaned ones
+
+
+def test_to_model_input_on_the_device(ctx):
+    import torch
+    from oracle import common as OC
+    rng = np.random.default_rng(7)
+    rgba = rng.integers(0, 256, size=(3, 28, 42, 4), dtype=np.uint8)
+    img = torch.empty(3, 3, 28, 42, device="cuda")
+    fg = torch.empty(3, 28, 42, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    ctx.to_model_input_device(rgba, img.data_ptr(), fg.data_ptr())
+    ctx.synchronize()
+    want_img, want_fg = OC.to_model_input(rgba)
+    assert np.array_equal(img.cpu().numpy(), want_img)          # same f32 operations, same order
+    assert np.array_equal(fg.cpu().numpy().astype(bool), want_fg)

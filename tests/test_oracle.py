@@ -367,3 +367,20 @@ def test_unprojection_projects_back_to_its_pixel():
 
 def test_f64_round_goes_away_from_zero():
     assert OG._round(np.array([2.5, -2.5, 0.4, -0.4, 1.5]).astype(np.float64)).tolist() == [3.0, -3.0, 0.0, -0.0, 2.0]
+
+
+def test_to_model_input_normalises_and_thresholds_alpha():
+    rgba = np.zeros((1, 2, 3, 4), np.uint8)
+    rgba[0, 0, 0] = [255, 255, 255, 128]
+    rgba[0, 0, 1] = [0, 0, 0, 127]
+    rgba[0, 1, 2] = [128, 64, 32, 255]
+    img, fg = C.to_model_input(rgba)
+    mean, std = np.array(specs.IMAGENET_MEAN), np.array(specs.IMAGENET_STD)
+    assert img.shape == (1, 3, 2, 3) and img.dtype == np.float32
+    assert np.allclose(img[0, :, 0, 0], (1 - mean) / std, atol=1e-6)
+    assert np.allclose(img[0, :, 0, 1], -mean / std, atol=1e-6)
+    assert np.allclose(img[0, :, 1, 2], (np.array([128, 64, 32]) / 255 - mean) / std, atol=1e-6)
+    assert fg.tolist() == [[[True, False, False], [False, False, True]]]
+    # the inverse of the normalisation used by the synthetic images returns the 8-bit values
+    back = (img * std[None, :, None, None] + mean[None, :, None, None]) * 255
+    assert np.allclose(back, rgba[..., :3].transpose(0, 3, 1, 2), atol=1e-3)
