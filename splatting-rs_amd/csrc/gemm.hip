@@ -442,18 +442,20 @@ template <int N> __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt v
 constexpr uint32_t OOB = 0x80000000u;
 
 template <int BM, int BN, int WM, int WN, int STAGES, int BK, int AMODE, bool RELU, int EPI>
-__global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
-  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+__global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32, NW = WM * WN;
   // A tile row holds BK bf16 = RB bytes = CPR 16-byte chunks; one load instruction of a wave
   // fills RPI rows (1 KiB). Chunk c of row r sits in slot c ^ ((r >> SH) & (CPR - 1)), which
   // keeps the 16 lanes of every ds_read_b128 phase on distinct banks.
   constexpr int RB = BK * 2, CPR = RB / 16, RPI = 64 / CPR, SH = CPR == 8 ? 1 : 2, KS = BK / 16;
   static_assert(BK == 64 || BK == 32, "k-tile");
-  constexpr int AL = BM / (4 * RPI), BL = BN / (4 * RPI);  // load instructions per wave per k-tile
+  constexpr int AL = BM / (NW * RPI), BL = BN / (NW * RPI);  // load instructions per wave per k-tile
   constexpr int LPT = AL + BL;
+  static_assert(AL * NW * RPI == BM && BL * NW * RPI == BN, "tile rows split evenly over the waves' loads");
+  static_assert(((NW * RPI) >> SH) % CPR == 0, "a load's swizzle slot is the same for every instruction");
   constexpr int STAGE = (BM + BN) * RB;
   static_assert((STAGES - 1) * LPT <= 63, "vmcnt range");
-  static_assert(STAGES * STAGE >= 4 * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the ring");
+  static_assert(STAGES * STAGE >= NW * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the ring");
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -482,7 +484,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
   uint32_t boff[BL];
 #pragma unroll
   for (int i = 0; i < BL; ++i) {
-    const long n = n0 + (i * 4 + wave) * RPI + lrow;
+    const long n = n0 + (i * NW + wave) * RPI + lrow;
     boff[i] = n < p.N ? uint32_t(n * p.ldw * 2 + c * 16) : OOB;
   }
   int32x4_t ra;
@@ -492,7 +494,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
     ra = make_rsrc(p.A, uint32_t(long(p.M) * p.lda * 2));
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
-      const long m = m0 + (i * 4 + wave) * RPI + lrow;
+      const long m = m0 + (i * NW + wave) * RPI + lrow;
       aoff[i] = m < p.M ? uint32_t(m * p.lda * 2 + c * 16) : OOB;
     }
   } else {
@@ -500,7 +502,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
     const int hw = p.Ho * p.Wo;
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
-      const long m = m0 + (i * 4 + wave) * RPI + lrow;
+      const long m = m0 + (i * NW + wave) * RPI + lrow;
       if (m < p.M) {
         const int v = int(m / hw), rem = int(m - long(v) * hw);
         const int oy = rem / p.Wo, ox = rem - oy * p.Wo;
@@ -524,17 +526,17 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const GemmArgs p, int ti
     if (l < AL) {
       const int i = l;
       if (AMODE == A_ROWS) {
-        load_to_lds(ra, (kin && aoff[i] != OOB) ? aoff[i] + kt * RB : OOB, sb + (i * 4 + wave) * 1024);
+        load_to_lds(ra, (kin && aoff[i] != OOB) ? aoff[i] + kt * RB : OOB, sb + (i * NW + wave) * 1024);
       } else {
         const int tap = k / p.Cin, ci = k - tap * p.Cin;
         const int ky = tap / p.ks, kx = tap - ky * p.ks;
         const int iy = aiy[i] + ky, ix = aix[i] + kx;
         const bool ok = kin && iy >= 0 && iy < p.Hi && ix >= 0 && ix < p.Wi;
-        load_to_lds(ra, ok ? aoff[i] + uint32_t((iy * p.Wi + ix) * p.Cin + ci) * 2 : OOB, sb + (i * 4 + wave) * 1024);
+        load_to_lds(ra, ok ? aoff[i] + uint32_t((iy * p.Wi + ix) * p.Cin + ci) * 2 : OOB, sb + (i * NW + wave) * 1024);
       }
     } else {
       const int i = l - AL;
-      load_to_lds(rw, (kin && boff[i] != OOB) ? boff[i] + kt * RB : OOB, sb + BM * RB + (i * 4 + wave) * 1024);
+      load_to_lds(rw, (kin && boff[i] != OOB) ? boff[i] + kt * RB : OOB, sb + BM * RB + (i * NW + wave) * 1024);
     }
   };
 
@@ -637,7 +639,7 @@ static void launch_bf16(const Exec& ex, const GemmArgs& a) {
   dim3 grid(tm * tn);
   const int epi = epi_kind(a);
 #define SPLAT_GO(AM, RL, EP) \
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(256), 0, ex.stream, a, tm, tn)
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(WM * WN * 64), 0, ex.stream, a, tm, tn)
   if (a.amode == A_ROWS) {
     if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
     else if (epi == EPI_RES) SPLAT_GO(A_ROWS, false, EPI_RES);
@@ -654,7 +656,10 @@ static void launch_bf16(const Exec& ex, const GemmArgs& a) {
 }
 
 // Tile choice: the fewest "rounds" of 256 CUs weighted by a per-tile cost relative to the
-// 256x256 tile (smaller tiles re-read more operand bytes through LDS per flop).
+// 256x256 tile (smaller tiles re-read more operand bytes through LDS per flop). The 256-row
+// tiles run 8 waves, two per SIMD: while one wave waits on its LDS reads the other issues
+// MFMAs, which the one-wave-per-SIMD form cannot hide (network shapes of the MapAnything C4
+// encoder, bias epilogue: 391 -> 331 us summed over one block's eight GEMMs).
 static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
   // Narrow outputs (the DA3 head's 32/64-channel convs): 128-row tiles and two stages keep the
   // LDS per block at 40-48 KB, so 3-4 blocks share a CU and hide each other's load latency
@@ -662,7 +667,7 @@ static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
   if (a.N <= 32) return launch_bf16<128, 32, 4, 1, 2>(ex, a);
   if (a.N <= 64) return launch_bf16<128, 64, 2, 2, 2>(ex, a);
   struct Cand { int bm, bn; double eff; };
-  const Cand cands[] = {{256, 256, 1.0}, {256, 128, 0.85}, {128, 128, 0.65}};
+  const Cand cands[] = {{256, 256, 1.0}, {256, 128, 0.80}, {128, 128, 0.65}};
   double best = 1e30;
   int pick = 0;
   for (int i = 0; i < 3; ++i) {
@@ -671,8 +676,8 @@ static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
     const double cost = double(rounds) * cands[i].bm * cands[i].bn / cands[i].eff;
     if (cost < best * 0.999) { best = cost; pick = i; }
   }
-  if (pick == 0) launch_bf16<256, 256, 2, 2, 2>(ex, a);
-  else if (pick == 1) launch_bf16<256, 128, 2, 2, 3>(ex, a);
+  if (pick == 0) launch_bf16<256, 256, 2, 4, 2>(ex, a);
+  else if (pick == 1) launch_bf16<256, 128, 4, 2, 3>(ex, a);
   else launch_bf16<128, 128, 2, 2, 4>(ex, a);
 }
 
