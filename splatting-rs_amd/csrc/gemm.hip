@@ -52,7 +52,18 @@ template <> struct Mfma<float> {
   }
 };
 
-__device__ inline float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+// Exact (erf) GELU, x * Phi(x). erfc(z) for z = |x|/sqrt(2) >= 0 follows Abramowitz & Stegun
+// 7.1.26: t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2) with t = 1/(1 + p z), absolute
+// error <= 1.5e-7. For x < 0 the result is 0.5 x erfc(z) directly, without the cancellation of
+// 1 + erf(x/sqrt(2)). About 20 VALU operations against the library erff's 30-40 (the GELU
+// epilogue is VALU-bound: 6222x4096 fc1 94.6 -> 77.1 us, 62.0 us without an activation).
+__device__ inline float gelu_erf(float x) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(1.f + 0.3275911f * z);
+  const float e = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f)))) *
+                  __expf(-z * z);
+  return x >= 0.f ? x - 0.5f * x * e : 0.5f * x * e;
+}
 
 // A residual is fp32 when flagged, else stored in the kernel's own dtype T.
 template <typename T>

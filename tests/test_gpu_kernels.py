@@ -64,6 +64,31 @@ def test_gemm_matches_torch(ctx, dtype, M, N, K, act):
     assert err2 < (1e-5 if dtype == "f32" else 8e-3), err2
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_gemm_gelu_epilogue_accuracy(ctx, dtype):
+    """The epilogue's GELU against the exact erf GELU over [-9, 9]: out[m, n] = x_m (A's first
+    column, W's first row of ones), so the GEMM adds no rounding and the check is the
+    activation's own error, <= 3e-7 * max(1, |x|) (erfc approximation error 1.5e-7, plus fp32
+    rounding)."""
+    code, tdt = _dt(dtype)
+    M, N, K = 4096, 64, 64
+    x = torch.linspace(-9, 9, M).to(tdt).double()
+    A = torch.zeros(M, K, dtype=tdt)
+    A[:, 0] = x.to(tdt)
+    Wm = torch.zeros(N, K, dtype=tdt)
+    Wm[:, 0] = 1
+    bias = torch.zeros(N)
+    dA, dW, db = A.cuda(), Wm.cuda(), bias.cuda()
+    out = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.kernel_gemm(code, dA.data_ptr(), M, K, dW.data_ptr(), N, K, db.data_ptr(), 2, out.data_ptr(), True)
+    ctx.synchronize()
+    ref = torch.nn.functional.gelu(x)[:, None].expand(M, N)
+    err = ((out.cpu().double() - ref).abs() / x.abs().clamp(min=1)[:, None]).max().item()
+    report("gemm.gelu", dtype=dtype, err=f"{err:.2e}")
+    assert err <= 3e-7, err
+
+
 ATTN_CASES = [
     # (S, L, heads)
     (1, 1, 1),
