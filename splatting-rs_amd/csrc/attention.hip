@@ -240,13 +240,15 @@ __global__ void __launch_bounds__(ATTN_WAVES * 64) attn_kernel(const AttnArgs p,
 
 // ---------------------------------------------------------------------------------------
 // bf16 main path. Each wave owns QT*32 queries, so every K and V^T fragment read from LDS
-// feeds QT matrix-core ops. K tiles stream straight into LDS (buffer_load_dwordx4 ... lds,
-// rows of 128 bytes with chunk c of row r in slot c ^ ((r >> 1) & 7)); V goes through
-// registers to be stored transposed. Rows past the sequence read as zero (buffer range check)
-// and are masked to -inf only in the last tile. The softmax keeps a reference max per query
-// and rescales O and the running sum only when a tile's max exceeds it by more than 2^8 (in
-// exp2 units): O and the sum always share the reference, so the result is exact and P stays
-// below 256.
+// feeds QT matrix-core ops. K and V tiles stream straight into LDS, row-major as they lie in
+// memory (buffer_load_dwordx4 ... lds, rows of 128 bytes = 64 head channels, XOR-swizzled by
+// 16-byte chunk). The V^T operand of O^T = V^T P^T is read with ds_read_b64_tr_b16, which
+// transposes 16-bit elements within each group of 16 lanes: no V pass through registers and no
+// VALU transpose (C4 global attention 239 -> 213 us). Rows past the sequence read as zero
+// (buffer range check) and are masked to -inf only in the last tile. The softmax keeps a
+// reference max per query and rescales O and the running sum only when a tile's max exceeds it
+// by more than 2^8 (in exp2 units): O and the sum always share the reference, so the result is
+// exact and P stays below 256.
 
 typedef int int32x4_t __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(3))) char* lds_cptr_a;
@@ -275,20 +277,13 @@ template <int N> __device__ inline void wait_vm() { asm volatile("s_waitcnt vmcn
 
 template <int WAVES, int QT>
 __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs p, float c) {
-  constexpr int NT = WAVES * 64;
-  constexpr int KBYTES = 64 * 128;            // K tile: 64 keys x 128 bytes, swizzled, unpadded
-  // V^T row: 64 keys (bf16) + 16 bytes (16-byte aligned rows, conflict-free 16-lane reads).
-  // Within every 16 keys the 4-key quads are stored in the order 0, 2, 1, 3, so that the 8
-  // keys one lane feeds the matrix core (quads g and g+2 of the 16) are 16 contiguous bytes.
-  constexpr int VROW = 64 * 2 + 16;
-  constexpr int VBYTES = 64 * VROW;
-  constexpr int KL = 8 / WAVES;               // K load instructions per wave per tile
-  constexpr int VB = 256 / NT;                // 4x4 V blocks per thread per tile
-  static_assert(WAVES == 2 || WAVES == 4, "the K-load swizzle assumes an even number of waves");
-  // LDS: two K tiles and two V^T tiles. K and V of tile t+1 are requested when tile t starts
-  // (V into registers, stored transposed when tile t is done). A deeper K ring measured no
-  // faster: the loop is bound by its VALU work, not by load latency.
-  __shared__ __attribute__((aligned(1024))) char smem[2 * KBYTES + 2 * VBYTES];
+  constexpr int KBYTES = 64 * 128;            // K or V tile: 64 keys x 128 bytes, swizzled, unpadded
+  constexpr int KL = 8 / WAVES;               // load instructions per wave per K (or V) tile
+  static_assert(WAVES == 2 || WAVES == 4, "the load swizzles assume an even number of waves");
+  // LDS: two K tiles, then two V tiles. K and V of tile t+1 are requested when tile t starts.
+  // A third stage measured slower (C4 global 224 vs 207 us): it costs occupancy, and the loop
+  // is bound by its VALU work, not by load latency.
+  __shared__ __attribute__((aligned(1024))) char smem[4 * KBYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -327,49 +322,42 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
       load_lds_a(rk, key < L ? uint32_t(key * p.ld * 2 + kc * 16) : 0x80000000u, sb + (i * WAVES + wave) * 1024);
     }
   };
-  // V rows through a buffer descriptor too: every load is issued (rows past the sequence read
-  // as zero), so the number of loads per tile, and with it each vmcnt wait, is fixed.
-  const __amdgpu_buffer_rsrc_t rvs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(V + base * p.ld), 0, int(long(L) * p.ld * 2), 0x00020000);
-  uint2 rv[VB][4];
-  int voff[VB][4];  // byte offset of this thread's V rows within a tile
+  // V rows: chunk c of row r in slot c ^ (2 * (r & 3)), so that the four consecutive rows one
+  // 16-lane group of a transposed read touches sit on four different 32-byte bank groups.
+  const bf16* Vseq = V + base * p.ld;
+  const int32x4_t rv = make_rsrc_a(Vseq, uint32_t(long(L) * p.ld * 2));
+  const int vc = (lane & 7) ^ ((lrow & 3) << 1);
+  auto issue_v = [&](int t, int buf) {
+    const uint32_t sb = uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_a)(smem + (2 + buf) * KBYTES)));
 #pragma unroll
-  for (int b = 0; b < VB; ++b)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int blk = tid + b * NT, kq = blk >> 4, dq = blk & 15;
-      voff[b][j] = ((4 * kq + j) * p.ld + 4 * dq) * 2;
-    }
-  auto load_v = [&](int t) {
-    const int tile_off = t * 64 * p.ld * 2;
-#pragma unroll
-    for (int b = 0; b < VB; ++b) {
-      const int kq = (tid + b * NT) >> 4;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = t * 64 + 4 * kq + j;
-        const auto w = __builtin_amdgcn_raw_buffer_load_b64(rvs, key < L ? tile_off + voff[b][j] : int(0x80000000u), 0, 0);
-        rv[b][j] = make_uint2(w[0], w[1]);
-      }
+    for (int i = 0; i < KL; ++i) {
+      const int row = (i * WAVES + wave) * 8 + lrow;
+      const int key = t * 64 + row;
+      load_lds_a(rv, key < L ? uint32_t(key * p.ld * 2 + vc * 16) : 0x80000000u, sb + (i * WAVES + wave) * 1024);
     }
   };
-  auto store_v = [&](int buf) {
-    char* vt = smem + 2 * KBYTES + buf * VBYTES;
+  // A operand of O^T[d][q] += V^T[d][keys] P^T[keys][q] for keys kt2*32 + 16*hh + (0..31): lane
+  // l supplies d = dt*32 + l%32 and, in the k order of the P fragment, keys kA..kA+3 and
+  // kA+8..kA+11 with kA = 16*hh + 4*(l/32). ds_read_b64_tr_b16 hands output lane i of a
+  // 16-lane group element i of the 16 consecutive elements that source lanes 4j..4j+3 of the
+  // group read, as its element j. So source lane s of group G reads row kA(G) + j (j = (s/4)%4)
+  // at head channels dt*32 + 16*(G&1) + 4*(s%4): group G holds d = dt*32 + 16*(G&1) + (0..15)
+  // and k-half G>>1.
+  const int G = lane >> 4, vj = (lane >> 2) & 3, vcc = lane & 3;
+  auto vfrag = [&](const char* vt, int kt2, int hh, int dt) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    uint32_t w[4];
 #pragma unroll
-    for (int b = 0; b < VB; ++b) {
-      const int blk = tid + b * NT, kq = blk >> 4, dq = blk & 15;
-      const uint16_t* e[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) e[j] = reinterpret_cast<const uint16_t*>(&rv[b][j]);
-#pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        uint2 w;
-        w.x = uint32_t(e[0][x]) | (uint32_t(e[1][x]) << 16);
-        w.y = uint32_t(e[2][x]) | (uint32_t(e[3][x]) << 16);
-        const int pq = (kq & ~3) | ((kq & 1) << 1) | ((kq >> 1) & 1);  // quad order 0, 2, 1, 3
-        *reinterpret_cast<uint2*>(vt + (4 * dq + x) * VROW + 8 * pq) = w;
-      }
+    for (int half = 0; half < 2; ++half) {
+      const int row = kt2 * 32 + 16 * hh + 8 * half + 4 * (G >> 1) + vj;
+      const int chunk = (4 * dt + 2 * (G & 1) + (vcc >> 1)) ^ ((row & 3) << 1);
+      const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4s*)((lds_cptr_a)(vt + row * 128 + chunk * 16 + (vcc & 1) * 8)));
+      const uint2 u = __builtin_bit_cast(uint2, r);
+      w[2 * half] = u.x;
+      w[2 * half + 1] = u.y;
     }
+    return make_uint4(w[0], w[1], w[2], w[3]);
   };
 
   f32x16 o[QT][2];
@@ -385,7 +373,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
 
   auto tile = [&](int t, int kbuf, int vbuf, bool masked) {
     const char* kb = smem + kbuf * KBYTES;
-    const char* vt = smem + 2 * KBYTES + vbuf * VBYTES;
+    const char* vt = smem + (2 + vbuf) * KBYTES;
     f32x16 s[QT][2];
     const f32x16 zero = {};
 #pragma unroll
@@ -419,7 +407,10 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
       for (int i = 0; i < 8; ++i)
         m8[i] = fmaxf(fmaxf(s[qt][0][2 * i], s[qt][0][2 * i + 1]), fmaxf(s[qt][1][2 * i], s[qt][1][2 * i + 1]));
       float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
-      mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+      // the other half of the query's keys sits in lane l ^ 32: one v_permlane32_swap gives
+      // every lane both halves (a ds_bpermute costs an LDS round trip)
+      const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw2[0]), __uint_as_float(sw2[1])) * c;
       mnew[qt] = mx > mref[qt] + 8.f ? mx : mref[qt];
       grow |= mnew[qt] != mref[qt];
     }
@@ -448,12 +439,11 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
     }
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
-      const char* vrow = vt + (dt * 32 + l32) * VROW;
 #pragma unroll
       for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const uint4 vf = *reinterpret_cast<const uint4*>(vrow + (kt2 * 32 + 16 * hh + 8 * g) * 2);
+          const uint4 vf = vfrag(vt, kt2, hh, dt);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {
             uint4 pf;
@@ -469,26 +459,23 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
   };
 
   const int ntiles = (L + 63) / 64;
-  constexpr int AFTER_K = 4 * VB;  // loads issued after a tile's K: its V
   issue_k(0, 0);
-  load_v(0);
-  store_v(0);
-  wait_vm<AFTER_K>();
+  issue_v(0, 0);
+  wait_vm<0>();
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    // K buffer (t+1)&1 held tile t-1; the V registers held tile t, already stored
+    // buffers (t+1)&1 held tile t-1, which every wave finished before the last barrier
     issue_k(t + 1, (t + 1) & 1);
-    load_v(t + 1);
+    issue_v(t + 1, (t + 1) & 1);
     tile(t, t & 1, t & 1, t + 1 == ntiles);
-    store_v((t + 1) & 1);
-    wait_vm<AFTER_K>();
+    wait_vm<0>();  // this wave's share of tile t+1 (zero-fill loads past the last tile included)
     __syncthreads();
   }
-  wait_vm<0>();  // the zero-fill loads past the last tile land before the block's LDS is released
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const float inv = 1.f / (lsum[qt] + __shfl_xor(lsum[qt], 32));
+    const auto l2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum[qt]), __float_as_uint(lsum[qt]), false, false);
+    const float inv = 1.f / (__uint_as_float(l2[0]) + __uint_as_float(l2[1]));
     const int qrow = q0 + qt * 32 + l32;
     if (qrow < L) {
       bf16* O = reinterpret_cast<bf16*>(p.o) + (base + qrow) * p.ldo + h * 64;
