@@ -315,6 +315,15 @@ int splat_ma_encode_device(splat_ctx* ctx, const float* images, int V, int H, in
   });
 }
 
+// A single GEMM outside a forward: a dry pass sizes its split-K workspace first.
+static void gemm_now(Context* c, const GemmArgs& g) {
+  Exec dry = c->ex;
+  dry.dry = true;
+  gemm(dry, g);
+  if (c->reserve_workspace()) c->clear_graphs();
+  gemm(c->ex, g);
+}
+
 int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, const void* W, int N, int ldw,
                       const float* bias, int act, void* out, int out_f32) {
   return guard(C(ctx), [&] {
@@ -334,7 +343,7 @@ int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, co
     g.out = out;
     g.ldc = N;
     g.out_f32 = out_f32;
-    gemm(C(ctx)->ex, g);
+    gemm_now(C(ctx), g);
   });
 }
 
@@ -419,7 +428,7 @@ int splat_kernel_conv2d(splat_ctx* ctx, int dtype, const void* in, int V, int H,
     g.act = act;
     g.res = res;
     g.ldres = Cout;
-    gemm(C(ctx)->ex, g);
+    gemm_now(C(ctx), g);
   });
 }
 
@@ -440,7 +449,7 @@ int splat_kernel_conv_transpose2d(splat_ctx* ctx, int dtype, const void* in, int
     u.ct_R = R;
     u.ct_C = Cc;
     u.ct_Cout = Cout;
-    gemm(C(ctx)->ex, u);
+    gemm_now(C(ctx), u);
   });
 }
 

@@ -90,12 +90,21 @@ struct Profiler {
   std::vector<ProfRecord> recs;
 };
 
+// Device scratch for split-K partial sums, owned by the context and shared by the launches
+// of its stream (one at a time). A dry run records in `need` the bytes the real run will ask
+// for; a launch splits only when `cap` covers its partials.
+struct Workspace {
+  void* ptr = nullptr;
+  size_t cap = 0, need = 0;
+};
+
 // Every launcher receives an Exec. With `dry` set, launchers only validate their arguments
-// and return: the forward runs once that way to size the activation arena.
+// and return: the forward runs once that way to size the activation arena (and `ws`).
 struct Exec {
   hipStream_t stream = nullptr;
   bool dry = false;
   Profiler* prof = nullptr;
+  Workspace* ws = nullptr;
 };
 
 // Records one launch when profiling: construct right before the launch, destroyed after it.

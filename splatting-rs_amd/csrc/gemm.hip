@@ -12,6 +12,7 @@
 // column l%32.
 #include "kernels.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace splat {
@@ -169,7 +170,9 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
 // LayerScale are loaded once, and the residuals of CH runs are requested before the first of
 // those runs is stored. `slab` is this wave's LDS region of 32 x slab_ld(TN) floats; the
 // block must be past its last read of the main-loop LDS.
-enum EpiKind { EPI_BIAS = 0, EPI_RES = 1, EPI_FULL = 2 };
+// EPI_PART: split-K slice, the raw fp32 sums go to the partial buffer; a reduce kernel adds
+// the slices and applies the full epilogue.
+enum EpiKind { EPI_BIAS = 0, EPI_RES = 1, EPI_FULL = 2, EPI_PART = 3 };
 
 constexpr int slab_ld(int tn) { return tn * 32 + 4; }  // +4 floats: conflict-free 16-byte row reads
 
@@ -200,9 +203,25 @@ __device__ __forceinline__ void read8(const float* q, float* v) {
 
 template <typename T, int TM, int TN, int EPI>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long wrow0, long wcol0, float* slab,
-                                         int lane, bool vec) {
+                                         int lane, bool vec, float* part = nullptr) {
   constexpr int COLS = TN * 32, LD = slab_ld(TN), RUNS = COLS / 8;
-  if constexpr (EPI == EPI_FULL) {
+  if constexpr (EPI == EPI_PART) {
+    // rows of 8 columns: n < N implies n + 8 <= ldp (ldp is N rounded up to 8)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      stage_slab<TM, TN>(acc, i, slab, lane);
+      for (int q = lane; q < 32 * RUNS; q += 64) {
+        const int rr = q / RUNS, cc = (q - rr * RUNS) * 8;
+        const long m = wrow0 + i * 32 + rr, n = wcol0 + cc;
+        if (m < p.M && n < p.N) {
+          float* dst = part + m * p.ldp + n;
+          *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(slab + rr * LD + cc);
+          *reinterpret_cast<float4*>(dst + 4) = *reinterpret_cast<const float4*>(slab + rr * LD + cc + 4);
+        }
+      }
+      slab_done();
+    }
+  } else if constexpr (EPI == EPI_FULL) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       stage_slab<TM, TN>(acc, i, slab, lane);
@@ -479,7 +498,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
   // dealt round-robin); otherwise the round-robin deal, which keeps one tile row per XCD and
   // measured the same time and less HBM traffic than contiguous runs on the network's shapes.
   const int nblk = tiles_m * tiles_n;
-  const int bid = (nblk & 7) == 0 ? xcd_contiguous(blockIdx.x, nblk) : blockIdx.x;
+  // split-K slices (EPI_PART): block b covers tile b % nblk over k-tiles [kt0, kt0 + nk)
+  const int split = EPI == EPI_PART ? int(blockIdx.x) / nblk : 0;
+  const int b0 = int(blockIdx.x) - split * nblk;
+  const int bid = (EPI != EPI_PART && (nblk & 7) == 0) ? xcd_contiguous(b0, nblk) : b0;
   const int per_group = 8 * tiles_n;
   const int first_m = (bid / per_group) * 8;
   const int gsize = min(tiles_m - first_m, 8);
@@ -528,12 +550,17 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
     }
   }
 
-  // Load instruction l (l < AL: A rows, else W rows) of k-tile kt into ring stage `stage`.
-  // K-chunks at or past K (tail and tiles beyond the last) read as zeros.
-  auto issue_one = [&](int kt, int stage, int l) {
+  const int nk_all = (p.K + BK - 1) / BK;
+  const int kt0 = split * p.kper;
+  const int nk = EPI == EPI_PART ? min(nk_all - kt0, p.kper) : nk_all;
+  const int kend = min(p.K, (kt0 + nk) * BK);
+  // Load instruction l (l < AL: A rows, else W rows) of k-tile kt0 + kr into ring stage
+  // `stage`. K-chunks at or past kend (tail and tiles beyond the slice) read as zeros.
+  auto issue_one = [&](int kr, int stage, int l) {
     const uint32_t sb = lds_addr(smem + stage * STAGE);
+    const int kt = kt0 + kr;
     const int k = kt * BK + c * 8;
-    const bool kin = k < p.K;
+    const bool kin = k < kend;
     if (l < AL) {
       const int i = l;
       if (AMODE == A_ROWS) {
@@ -561,7 +588,6 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
 
   const int sw = (l32 >> SH) & (CPR - 1);  // fragment rows are l32 plus multiples of 32
   const int arow0 = (wm * (BM / WM) + l32) * RB, brow0 = (BM + wn * (BN / WN) + l32) * RB;
-  const int nk = (p.K + BK - 1) / BK;
   // Prologue: STAGES tiles in flight, tile 0 resident for every wave, its first fragments read.
   // Every k-tile slot is loaded, also past the last tile (as zeros), so that the number of
   // loads in flight, and with it each vmcnt wait, is the same for every tile.
@@ -641,17 +667,50 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
   wait_vmcnt<0>();  // the zero-fill loads past the last tile must land before the ring is reused
   __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
   float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
-  epilogue<bf16, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec);
+  epilogue<bf16, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
+                              EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr);
 }
 
+// Split-K reduction: out = epilogue(sum over slices of the fp32 partials), 8 columns a thread.
+template <typename T>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p, int S) {
+  const long runs = (p.N + 7) / 8;
+  const long id = long(blockIdx.x) * 256 + threadIdx.x;
+  if (id >= long(p.M) * runs) return;
+  const long m = id / runs, n = (id - m * runs) * 8;
+  const long stride = long(p.M) * p.ldp;
+  const float* src = p.part + m * p.ldp + n;
+  float v[8];
+  read8(src, v);
+  for (int s = 1; s < S; ++s) {
+    float w[8];
+    read8(src + s * stride, w);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] += w[k];
+  }
+  epi8<T>(p, v, m, n, p.epi_vec && n + 8 <= p.N);
+}
+
+constexpr int GEMM_CUS = 256;  // MI355X compute units: one "round" of resident blocks per CU slot
+
 template <int BM, int BN, int WM, int WN, int STAGES, int BK = 64>
-static void launch_bf16(const Exec& ex, const GemmArgs& a) {
+static void launch_bf16(const Exec& ex, const GemmArgs& a, int S) {
   const int tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
-  dim3 grid(tm * tn);
-  const int epi = epi_kind(a);
+  const int epi = S > 1 ? EPI_PART : epi_kind(a);
+  GemmArgs b = a;
+  if (S > 1) {
+    b.part = static_cast<float*>(ex.ws->ptr);
+    b.ldp = (a.N + 7) / 8 * 8;
+    b.kper = cdiv(cdiv(a.K, BK), S);
+  }
+  dim3 grid(tm * tn * S);
 #define SPLAT_GO(AM, RL, EP) \
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(WM * WN * 64), 0, ex.stream, a, tm, tn)
-  if (a.amode == A_ROWS) {
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(WM * WN * 64), 0, ex.stream, b, tm, tn)
+  if (epi == EPI_PART) {
+    if (a.amode == A_ROWS) SPLAT_GO(A_ROWS, false, EPI_PART);
+    else if (a.relu_in) SPLAT_GO(A_CONV, true, EPI_PART);
+    else SPLAT_GO(A_CONV, false, EPI_PART);
+  } else if (a.amode == A_ROWS) {
     if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
     else if (epi == EPI_RES) SPLAT_GO(A_ROWS, false, EPI_RES);
     else SPLAT_GO(A_ROWS, false, EPI_FULL);
@@ -664,6 +723,24 @@ static void launch_bf16(const Exec& ex, const GemmArgs& a) {
   }
 #undef SPLAT_GO
   SPLAT_HIP(hipGetLastError());
+  if (S > 1) {
+    const long work = long(a.M) * ((a.N + 7) / 8);
+    hipLaunchKernelGGL(splitk_reduce_kernel<bf16>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b, S);
+    SPLAT_HIP(hipGetLastError());
+  }
+}
+
+// Tile configurations of the bf16 path: block tile, and how many blocks share a CU.
+enum BfCfg { CFG_128x32, CFG_128x64, CFG_256x256, CFG_256x128, CFG_128x128 };
+struct BfShape { int bm, bn, per_cu; };
+static BfShape bf_shape(BfCfg c) {
+  switch (c) {
+    case CFG_128x32: return {128, 32, 3};
+    case CFG_128x64: return {128, 64, 3};
+    case CFG_256x256: return {256, 256, 1};
+    case CFG_256x128: return {256, 128, 1};
+    default: return {128, 128, 1};
+  }
 }
 
 // Tile choice: the fewest "rounds" of 256 CUs weighted by a per-tile cost relative to the
@@ -671,25 +748,55 @@ static void launch_bf16(const Exec& ex, const GemmArgs& a) {
 // tiles run 8 waves, two per SIMD: while one wave waits on its LDS reads the other issues
 // MFMAs, which the one-wave-per-SIMD form cannot hide (network shapes of the MapAnything C4
 // encoder, bias epilogue: 391 -> 331 us summed over one block's eight GEMMs).
-static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
+static BfCfg pick_bf16(const GemmArgs& a) {
   // Narrow outputs (the DA3 head's 32/64-channel convs): 128-row tiles and two stages keep the
   // LDS per block at 40-48 KB, so 3-4 blocks share a CU and hide each other's load latency
   // (C2 convs 475 -> 266 us against 256-row tiles with 3-4 stages).
-  if (a.N <= 32) return launch_bf16<128, 32, 4, 1, 2>(ex, a);
-  if (a.N <= 64) return launch_bf16<128, 64, 2, 2, 2>(ex, a);
-  struct Cand { int bm, bn; double eff; };
-  const Cand cands[] = {{256, 256, 1.0}, {256, 128, 0.80}, {128, 128, 0.65}};
+  if (a.N <= 32) return CFG_128x32;
+  if (a.N <= 64) return CFG_128x64;
+  const BfCfg cands[] = {CFG_256x256, CFG_256x128, CFG_128x128};
+  const double eff[] = {1.0, 0.80, 0.65};
   double best = 1e30;
-  int pick = 0;
+  BfCfg pick = CFG_256x256;
   for (int i = 0; i < 3; ++i) {
-    const long tiles = long(cdiv(a.M, cands[i].bm)) * cdiv(a.N, cands[i].bn);
-    const long rounds = (tiles + 255) / 256;
-    const double cost = double(rounds) * cands[i].bm * cands[i].bn / cands[i].eff;
-    if (cost < best * 0.999) { best = cost; pick = i; }
+    const BfShape sh = bf_shape(cands[i]);
+    const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
+    const long rounds = (tiles + GEMM_CUS - 1) / GEMM_CUS;
+    const double cost = double(rounds) * sh.bm * sh.bn / eff[i];
+    if (cost < best * 0.999) { best = cost; pick = cands[i]; }
   }
-  if (pick == 0) launch_bf16<256, 256, 2, 4, 2>(ex, a);
-  else if (pick == 1) launch_bf16<256, 128, 4, 2, 3>(ex, a);
-  else launch_bf16<128, 128, 2, 2, 4>(ex, a);
+  return pick;
+}
+
+// Split-K: a launch whose tiles fill less than half of one round of block slots and whose K
+// spans at least 16 k-tiles is cut into S >= 2 slices of at least 8 k-tiles, S * tiles within
+// one round. The slices write fp32 partials; a second kernel sums them and applies the
+// epilogue (the DPT head's coarse-level convs: M = 1596, K = 6912, 14 tiles of 256x128).
+static int split_factor(const GemmArgs& a, BfCfg c) {
+  const BfShape sh = bf_shape(c);
+  const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
+  const long slots = long(GEMM_CUS) * sh.per_cu;
+  const int nk = cdiv(a.K, 64);
+  if (2 * tiles > slots || nk < 16) return 1;
+  const int S = int(std::min<long>(nk / 8, slots / tiles));
+  if (S < 2) return 1;
+  return cdiv(nk, cdiv(nk, S));  // every slice non-empty
+}
+static size_t split_bytes(const GemmArgs& a, int S) {
+  return S > 1 ? size_t(S) * a.M * ((a.N + 7) / 8 * 8) * sizeof(float) : 0;
+}
+
+static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
+  const BfCfg c = pick_bf16(a);
+  int S = split_factor(a, c);
+  if (S > 1 && !(ex.ws && ex.ws->ptr && ex.ws->cap >= split_bytes(a, S))) S = 1;
+  switch (c) {
+    case CFG_128x32: return launch_bf16<128, 32, 4, 1, 2>(ex, a, S);
+    case CFG_128x64: return launch_bf16<128, 64, 2, 2, 2>(ex, a, S);
+    case CFG_256x256: return launch_bf16<256, 256, 2, 4, 2>(ex, a, S);
+    case CFG_256x128: return launch_bf16<256, 128, 4, 2, 3>(ex, a, S);
+    default: return launch_bf16<128, 128, 2, 2, 4>(ex, a, S);
+  }
 }
 
 template <typename T, int BM, int BN, int WM, int WN>
@@ -702,11 +809,16 @@ static void launch_cfg(const Exec& ex, const GemmArgs& a) {
   SPLAT_HIP(hipGetLastError());
 }
 
+// The MFMA bf16 path addresses its operands with 32-bit buffer offsets.
+static bool bf16_path_ok(const GemmArgs& a) {
+  const double abytes = a.amode == A_ROWS ? double(a.M) * a.lda * 2 : double(a.V) * a.Hi * a.Wi * a.Cin * 2;
+  return a.dt == BF16 && abytes < 2147483648.0 && double(a.N) * a.ldw * 2 < 2147483648.0;
+}
+
 template <typename T>
 static void launch_typed(const Exec& ex, const GemmArgs& a) {
   if constexpr (sizeof(T) == 2) {
-    const double abytes = a.amode == A_ROWS ? double(a.M) * a.lda * 2 : double(a.V) * a.Hi * a.Wi * a.Cin * 2;
-    if (abytes < 2147483648.0 && double(a.N) * a.ldw * 2 < 2147483648.0) return launch_bf16_auto(ex, a);
+    if (bf16_path_ok(a)) return launch_bf16_auto(ex, a);
   }
   const long tiles128 = (long)cdiv(a.M, 128) * cdiv(a.N, 128);
   if (a.N <= 32) launch_cfg<T, 256, 32, 4, 1>(ex, a);
@@ -732,6 +844,8 @@ void gemm(const Exec& ex, const GemmArgs& args) {
   if (a.store == STORE_CONVT)
     SPLAT_CHECK((long)a.ct_s * a.ct_s * a.ct_Cout == a.N && (long)a.V * a.ct_R * a.ct_C == a.M, BAD_ARGUMENT,
                 "gemm: convT geometry");
+  if (ex.dry && ex.ws && a.M > 0 && bf16_path_ok(a))  // size the split-K partials of the real run
+    ex.ws->need = std::max(ex.ws->need, split_bytes(a, split_factor(a, pick_bf16(a))));
   if (ex.dry || a.M == 0) return;
   const double es = a.dt == F32 ? 4 : 2, mn = double(a.M) * a.N;
   const double abytes = a.amode == A_ROWS ? double(a.M) * a.K * es : double(a.V) * a.Hi * a.Wi * a.Cin * es;

@@ -44,6 +44,8 @@ struct GemmArgs {
   int store = STORE_ROWS;
   int ct_s = 1, ct_R = 0, ct_C = 0, ct_Cout = 0;
   int epi_vec = 0;  // set by gemm(): the epilogue may use 16-byte vector accesses
+  // Set by gemm() for a split-K launch: fp32 partial sums [splits][M][ldp], kper k-tiles each.
+  float* part = nullptr; long ldp = 0; int kper = 0;
 };
 void gemm(const Exec& ex, const GemmArgs& a);
 

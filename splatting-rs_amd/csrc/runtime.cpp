@@ -503,6 +503,18 @@ Context::Context(int dev) : device(dev) {
   SPLAT_HIP(hipSetDevice(dev));
   SPLAT_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   ex.stream = stream;
+  ex.ws = &ws;
+}
+
+bool Context::reserve_workspace() {
+  if (ws.need <= ws.cap) return false;
+  SPLAT_HIP(hipStreamSynchronize(stream));
+  if (ws.ptr) SPLAT_HIP(hipFree(ws.ptr));
+  ws.ptr = nullptr;
+  ws.cap = 0;
+  SPLAT_HIP(hipMalloc(&ws.ptr, ws.need));
+  ws.cap = ws.need;
+  return true;
 }
 
 Context::~Context() {
@@ -513,6 +525,7 @@ Context::~Context() {
   ma.reset();
   for (auto& kv : staging)
     if (kv.second.first) (void)hipFree(kv.second.first);
+  if (ws.ptr) (void)hipFree(ws.ptr);
   if (stream) (void)hipStreamDestroy(stream);
 }
 

@@ -260,6 +260,10 @@ class Context {
   Exec ex;
   DevicePool pool;
   Arena arena;
+  Workspace ws;
+  // Grows `ws` to ws.need (synchronises the stream first; the old buffer may be in use).
+  // True if the buffer moved, which invalidates captured graphs.
+  bool reserve_workspace();
   std::string last_error;
   bool graphs = false;
   Hooks hooks;
@@ -303,6 +307,7 @@ void Context::run(const GraphKey& key, bool use_graph, F&& body) {
   body();
   ex.dry = false;
   if (arena.reserve(arena.peak())) clear_graphs();
+  if (reserve_workspace()) clear_graphs();
   arena.begin(false);
   if (!use_graph) {
     body();

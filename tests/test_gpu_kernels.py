@@ -26,6 +26,10 @@ GEMM_CASES = [
     (5838, 384, 1536, 0),
     (129, 130, 784, 1),
     (2500, 3072, 1024, 2),
+    # split-K (fewer tiles than half a round of CUs, K >= 16 k-tiles): fp32 partials + reduce
+    (100, 256, 4096, 0),
+    (777, 64, 2048, 2),
+    (300, 1001, 2048, 1),
 ]
 
 
@@ -135,6 +139,9 @@ CONV_CASES = [
     (3, 13, 9, 32, 7, 3, 1, 0, 1, False),
     (2, 10, 11, 96, 256, 1, 1, 0, 0, True),
     (1, 28, 37, 256, 128, 3, 1, 0, 0, False),
+    # split-K: the DPT head's coarsest level (M = 1596, K = 6912) and a narrow conv
+    (6, 19, 14, 768, 256, 3, 1, 0, 0, True),
+    (2, 9, 7, 512, 64, 3, 1, 1, 1, False),
 ]
 
 
