@@ -26,6 +26,7 @@ GEMM_CASES = [
     (5838, 384, 1536, 0),
     (129, 130, 784, 1),
     (2500, 3072, 1024, 2),
+    (6000, 3072, 1024, 2),  # 320x128 tiles (456 tiles: two rounds of 256 CUs)
     # split-K (fewer tiles than half a round of CUs, K >= 16 k-tiles): fp32 partials + reduce
     (100, 256, 4096, 0),
     (777, 64, 2048, 2),
