@@ -731,7 +731,7 @@ static void launch_bf16(const Exec& ex, const GemmArgs& a, int S) {
 }
 
 // Tile configurations of the bf16 path: block tile, and how many blocks share a CU.
-enum BfCfg { CFG_128x32, CFG_128x64, CFG_256x256, CFG_256x128, CFG_320x128, CFG_128x128 };
+enum BfCfg { CFG_128x32, CFG_128x64, CFG_256x256, CFG_256x128, CFG_320x256, CFG_320x128, CFG_192x128, CFG_128x128 };
 struct BfShape { int bm, bn, per_cu; };
 static BfShape bf_shape(BfCfg c) {
   switch (c) {
@@ -739,7 +739,9 @@ static BfShape bf_shape(BfCfg c) {
     case CFG_128x64: return {128, 64, 3};
     case CFG_256x256: return {256, 256, 1};
     case CFG_256x128: return {256, 128, 1};
+    case CFG_320x256: return {320, 256, 1};
     case CFG_320x128: return {320, 128, 1};
+    case CFG_192x128: return {192, 128, 1};
     default: return {128, 128, 1};
   }
 }
@@ -748,20 +750,23 @@ static BfShape bf_shape(BfCfg c) {
 // 256x256 tile (smaller tiles re-read more operand bytes through LDS per flop). The 256-row
 // tiles run 8 waves, two per SIMD: while one wave waits on its LDS reads the other issues
 // MFMAs, which the one-wave-per-SIMD form cannot hide (network shapes of the MapAnything C4
-// encoder, bias epilogue: 391 -> 331 us summed over one block's eight GEMMs). 320x128 (8 waves
-// of 160x32, 2 stages) exists for M = 6222-row shapes whose 256-row tiles leave a third round
-// mostly empty: 480 tiles fill two rounds (QKV 6222x3072x1024 59.5 -> 48.5 us).
+// encoder, bias epilogue: 391 -> 331 us summed over one block's eight GEMMs). The other
+// shapes exist for the round count at M = 5838-6223 rows, where 256-row tiles leave a last
+// round mostly empty: 320x256 (8 waves of 160x64, 2 stages) puts 6222x3072 in one round of 240
+// tiles (QKV 6222x3072x1024: 59.5 us as 600 tiles of 256x128, 48.5 as 480 of 320x128, 42.3);
+// 192x128 (8 waves of 96x32, 3 stages) puts N = 768 in one round of 198 smaller tiles
+// (6223x768x3072 42.4 -> 38.4 us).
 static BfCfg pick_bf16(const GemmArgs& a) {
   // Narrow outputs (the DA3 head's 32/64-channel convs): 128-row tiles and two stages keep the
   // LDS per block at 40-48 KB, so 3-4 blocks share a CU and hide each other's load latency
   // (C2 convs 475 -> 266 us against 256-row tiles with 3-4 stages).
   if (a.N <= 32) return CFG_128x32;
   if (a.N <= 64) return CFG_128x64;
-  const BfCfg cands[] = {CFG_256x256, CFG_256x128, CFG_320x128, CFG_128x128};
-  const double eff[] = {1.0, 0.80, 0.80, 0.65};
+  const BfCfg cands[] = {CFG_256x256, CFG_256x128, CFG_320x256, CFG_320x128, CFG_192x128, CFG_128x128};
+  const double eff[] = {1.0, 0.80, 1.0, 0.80, 0.75, 0.65};
   double best = 1e30;
   BfCfg pick = CFG_256x256;
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 6; ++i) {
     const BfShape sh = bf_shape(cands[i]);
     const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
     const long rounds = (tiles + GEMM_CUS - 1) / GEMM_CUS;
@@ -798,7 +803,9 @@ static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
     case CFG_128x64: return launch_bf16<128, 64, 2, 2, 2>(ex, a, S);
     case CFG_256x256: return launch_bf16<256, 256, 2, 4, 2>(ex, a, S);
     case CFG_256x128: return launch_bf16<256, 128, 4, 2, 3>(ex, a, S);
+    case CFG_320x256: return launch_bf16<320, 256, 2, 4, 2>(ex, a, S);
     case CFG_320x128: return launch_bf16<320, 128, 2, 4, 2>(ex, a, S);
+    case CFG_192x128: return launch_bf16<192, 128, 2, 4, 3>(ex, a, S);
     default: return launch_bf16<128, 128, 2, 2, 4>(ex, a, S);
   }
 }

@@ -26,7 +26,9 @@ GEMM_CASES = [
     (5838, 384, 1536, 0),
     (129, 130, 784, 1),
     (2500, 3072, 1024, 2),
-    (6000, 3072, 1024, 2),  # 320x128 tiles (456 tiles: two rounds of 256 CUs)
+    (6000, 3072, 1024, 2),  # 320x256 tiles (228: one round of 256 CUs)
+    (6000, 1536, 512, 1),   # 320x128 tiles (228)
+    (6000, 768, 768, 0),    # 192x128 tiles (192)
     # split-K (fewer tiles than half a round of CUs, K >= 16 k-tiles): fp32 partials + reduce
     (100, 256, 4096, 0),
     (777, 64, 2048, 2),
