@@ -3,6 +3,8 @@
 // DA3 reference-view selection and hook assembly, and elementwise helpers.
 #include "kernels.h"
 
+#include <algorithm>
+
 namespace splat {
 
 namespace {
@@ -487,8 +489,85 @@ __global__ void pw_coop_kernel(int mode, const void* in, long pix, int hw, int c
   }
 }
 
+// MapAnything head on 128-channel pixels: 8 lanes per pixel, each holding 16 channels and
+// their 6x16 weights in registers (loaded once, then a grid-stride loop over pixels, two per
+// lane group per trip so that two loads are in flight). The 6 dot products are summed across
+// the 8 lanes with DPP (the two quad swaps, then the half-row mirror), which leaves all 6 sums
+// in every lane, and the lanes share the pixel's stores.
+template <int CTRL> __device__ inline float dpp_add(float v) {
+  const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true);
+  return v + __int_as_float(o);
+}
+template <typename T>
+__global__ void __launch_bounds__(256) pw_ma128_kernel(const void* in, long pix, int hw, const float* w, const float* b,
+                                                       float* o0, float* o1, float* o2, uint8_t* o3, const float* scale) {
+  constexpr int UNROLL = 2;
+  const int sub = threadIdx.x & 7, c0 = sub * 16;
+  float wr[6][16];
+#pragma unroll
+  for (int o = 0; o < 6; ++o)
+#pragma unroll
+    for (int k = 0; k < 16; ++k) wr[o][k] = w[o * 128 + c0 + k];
+  float bo[6];
+#pragma unroll
+  for (int o = 0; o < 6; ++o) bo[o] = b[o];
+  const float sc = scale ? *scale : 1.f;
+  const long groups = long(gridDim.x) * blockDim.x / 8;
+  for (long base = (long(blockIdx.x) * blockDim.x + threadIdx.x) / 8; base < pix; base += groups * UNROLL) {
+    float x[UNROLL][16];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const long px = base + u * groups;
+#pragma unroll
+      for (int k = 0; k < 16; k += 4) {
+        const float4 f = px < pix ? ld4<T>(in, px * 128 + c0 + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        x[u][k] = f.x; x[u][k + 1] = f.y; x[u][k + 2] = f.z; x[u][k + 3] = f.w;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const long px = base + u * groups;
+      float acc[6];
+#pragma unroll
+      for (int o = 0; o < 6; ++o) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) s += wr[o][k] * x[u][k];
+        s = dpp_add<0xB1>(s);   // quad_perm [1,0,3,2]
+        s = dpp_add<0x4E>(s);   // quad_perm [2,3,0,1]
+        s = dpp_add<0x141>(s);  // row_half_mirror: the other quad of the 8
+        acc[o] = s + bo[o];
+      }
+      if (px >= pix) continue;  // uniform across the pixel's 8 lanes
+      const long v = px / hw, q = px - v * hw;
+      float mine = acc[0];
+#pragma unroll
+      for (int o = 1; o < 6; ++o) mine = sub == o ? acc[o] : mine;
+      if (o0 && sub < 6) o0[(v * 6 + sub) * hw + q] = mine;
+      // mapanything-rs/src/model.rs:155-168
+      const float nrm = fmaxf(sqrtf(acc[0] * acc[0] + acc[1] * acc[1] + acc[2] * acc[2]), 1e-8f);
+      const float depth = expf(acc[3]) * sc;
+      if (o1 && sub < 3) o1[px * 3 + sub] = mine / nrm * depth;
+      if (o2 && sub == 6) o2[px] = 1.f + expf(acc[4]);
+      if (o3 && sub == 7) o3[px] = acc[5] > 0.f ? 1 : 0;
+    }
+  }
+}
+
 void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, int hw, int cin, int cout,
                     const float* w, const float* b, float* o0, float* o1, float* o2, uint8_t* o3, const float* scale) {
+  if (mode == PW_MA && cin == 128 && cout == 6 && !ex.dry && pix > 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0) {
+    const double obytes = (o0 ? 24.0 : 0) + (o1 ? 12.0 : 0) + (o2 ? 4.0 : 0) + (o3 ? 1.0 : 0);
+    ProfScope ps(ex, "pointwise_head", 2.0 * pix * cin * cout, double(pix) * (cin * dtype_size(dt) + obytes));
+    // about three 256-thread blocks per CU, each lane group walking many pixels
+    const long blocks = std::min<long>(cdiv(pix * 8, 256), 256L * 3);
+    if (dt == F32)
+      hipLaunchKernelGGL(pw_ma128_kernel<float>, dim3(blocks), dim3(256), 0, ex.stream, in, pix, hw, w, b, o0, o1, o2, o3, scale);
+    else
+      hipLaunchKernelGGL(pw_ma128_kernel<bf16>, dim3(blocks), dim3(256), 0, ex.stream, in, pix, hw, w, b, o0, o1, o2, o3, scale);
+    SPLAT_HIP(hipGetLastError());
+    return;
+  }
   if ((cin == 32 || cin == 64 || cin == 128) && !ex.dry && pix > 0 && cout <= 8 &&
       (reinterpret_cast<uintptr_t>(in) & 15) == 0) {
     SPLAT_CHECK(mode != PW_DEPTH || cout == 2, BAD_ARGUMENT, "depth head has 2 channels");
