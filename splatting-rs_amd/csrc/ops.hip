@@ -300,45 +300,74 @@ __global__ void resize_kernel(const void* in, int V, int Hi, int Wi, int C, void
 }
 
 // Same, 8 channels per thread (C % 8 == 0): the four source pixels and the output are read
-// and written as 8-channel vectors.
+// and written as 8-channel vectors (one 16-byte access per pixel for bf16). One block row per
+// output row (grid.y = V*Ho), so the row's source rows and weight follow from blockIdx.y and the
+// per-thread index math is 32-bit (C4's five resizes 295 -> 230 us against a flat 64-bit index
+// decomposition with 8-byte accesses).
+template <typename T> struct Vec8;
+template <> struct Vec8<bf16> {
+  __device__ static inline void load(const void* p, long i, float* v) {
+    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(p) + i);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = bf2f(bf16(w[k] & 0xffffu));
+      v[2 * k + 1] = bf2f(bf16(w[k] >> 16));
+    }
+  }
+  __device__ static inline void store(void* p, long i, const float* v) {
+    uint4 u;
+    u.x = pack_bf16x2(v[0], v[1]);
+    u.y = pack_bf16x2(v[2], v[3]);
+    u.z = pack_bf16x2(v[4], v[5]);
+    u.w = pack_bf16x2(v[6], v[7]);
+    *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p) + i) = u;
+  }
+};
+template <> struct Vec8<float> {
+  __device__ static inline void load(const void* p, long i, float* v) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  __device__ static inline void store(void* p, long i, const float* v) {
+    float* o = reinterpret_cast<float*>(p) + i;
+    *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
 template <typename T>
-__global__ void resize8_kernel(const void* in, int V, int Hi, int Wi, int C, void* out, int Hf, int Wf, int Ho, int Wo,
-                               const float* addtab, int relu) {
-  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void __launch_bounds__(256) resize8_kernel(const void* in, int Hi, int Wi, int C, void* out, int Hf, int Wf,
+                                                      int Ho, int Wo, const float* addtab, int relu) {
   const int C8 = C >> 3;
-  const long total = (long)V * Ho * Wo * C8;
-  if (id >= total) return;
-  const int c = int(id % C8) * 8;
-  long r = id / C8;
-  const int ox = int(r % Wo);
-  r /= Wo;
-  const int oy = int(r % Ho);
-  const long v = r / Ho;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= Wo * C8) return;
+  const int row = blockIdx.y, v = row / Ho, oy = row - v * Ho;
+  const int ox = t / C8, c = (t - ox * C8) * 8;
   const double fy = Hf > 1 ? double(Hi - 1) * oy / double(Hf - 1) : 0.0;
   const double fx = Wf > 1 ? double(Wi - 1) * ox / double(Wf - 1) : 0.0;
   const int y0 = min(int(fy), Hi - 1), x0 = min(int(fx), Wi - 1);
   const int y1 = y0 + (y0 < Hi - 1 ? 1 : 0), x1 = x0 + (x0 < Wi - 1 ? 1 : 0);
   const float ly = float(fy - y0), lx = float(fx - x0);
-  const long b = v * Hi * Wi;
-  const long i00 = (b + (long)y0 * Wi + x0) * C + c, i01 = (b + (long)y0 * Wi + x1) * C + c;
-  const long i10 = (b + (long)y1 * Wi + x0) * C + c, i11 = (b + (long)y1 * Wi + x1) * C + c;
-  const long o = id * 8;
+  const long b = long(v) * Hi * Wi;
+  float a[8], bq[8], cq[8], d[8], y[8];
+  Vec8<T>::load(in, (b + long(y0) * Wi + x0) * C + c, a);
+  Vec8<T>::load(in, (b + long(y0) * Wi + x1) * C + c, bq);
+  Vec8<T>::load(in, (b + long(y1) * Wi + x0) * C + c, cq);
+  Vec8<T>::load(in, (b + long(y1) * Wi + x1) * C + c, d);
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float4 a = ld4<T>(in, i00 + 4 * h), bq = ld4<T>(in, i01 + 4 * h);
-    const float4 cq = ld4<T>(in, i10 + 4 * h), d = ld4<T>(in, i11 + 4 * h);
-    float4 y;
-    y.x = (1.f - ly) * ((1.f - lx) * a.x + lx * bq.x) + ly * ((1.f - lx) * cq.x + lx * d.x);
-    y.y = (1.f - ly) * ((1.f - lx) * a.y + lx * bq.y) + ly * ((1.f - lx) * cq.y + lx * d.y);
-    y.z = (1.f - ly) * ((1.f - lx) * a.z + lx * bq.z) + ly * ((1.f - lx) * cq.z + lx * d.z);
-    y.w = (1.f - ly) * ((1.f - lx) * a.w + lx * bq.w) + ly * ((1.f - lx) * cq.w + lx * d.w);
-    if (addtab) {
-      const float4 t = *reinterpret_cast<const float4*>(addtab + ((long)oy * Wo + ox) * C + c + 4 * h);
-      y.x += t.x; y.y += t.y; y.z += t.z; y.w += t.w;
-    }
-    if (relu) { y.x = fmaxf(y.x, 0.f); y.y = fmaxf(y.y, 0.f); y.z = fmaxf(y.z, 0.f); y.w = fmaxf(y.w, 0.f); }
-    st4<T>(out, o + 4 * h, y);
+  for (int k = 0; k < 8; ++k) y[k] = (1.f - ly) * ((1.f - lx) * a[k] + lx * bq[k]) + ly * ((1.f - lx) * cq[k] + lx * d[k]);
+  if (addtab) {
+    const float* tp = addtab + (long(oy) * Wo + ox) * C + c;
+    const float4 t0 = *reinterpret_cast<const float4*>(tp), t1 = *reinterpret_cast<const float4*>(tp + 4);
+    y[0] += t0.x; y[1] += t0.y; y[2] += t0.z; y[3] += t0.w; y[4] += t1.x; y[5] += t1.y; y[6] += t1.z; y[7] += t1.w;
   }
+  if (relu) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) y[k] = fmaxf(y[k], 0.f);
+  }
+  Vec8<T>::store(out, (long(row) * Wo + ox) * C + c, y);
 }
 
 void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int Wi, int C, void* out, int Hf, int Wf,
@@ -349,9 +378,10 @@ void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int 
   if (C % 8 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(addtab) & 15) == 0) {
     ProfScope ps(ex, "resize_bilinear", 0, (double(V) * Hi * Wi * C + double(total)) * dtype_size(dt) + (addtab ? double(Ho) * Wo * C * 4 : 0));
-    dim3 grid(cdiv(total / 8, 256));
-    if (dt == F32) hipLaunchKernelGGL(resize8_kernel<float>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
-    else hipLaunchKernelGGL(resize8_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+    SPLAT_CHECK(long(Wo) * (C / 8) < (1L << 31) && long(V) * Ho < 65536, BAD_ARGUMENT, "resize: grid");
+    dim3 grid(cdiv(long(Wo) * (C / 8), 256), V * Ho);
+    if (dt == F32) hipLaunchKernelGGL(resize8_kernel<float>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+    else hipLaunchKernelGGL(resize8_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
     SPLAT_HIP(hipGetLastError());
     return;
   }
