@@ -12,10 +12,24 @@ namespace {
 template <typename T> __device__ inline float ld(const void* p, long i) { return to_f<T>(reinterpret_cast<const T*>(p)[i]); }
 template <typename T> __device__ inline void st(void* p, long i, float v) { reinterpret_cast<T*>(p)[i] = from_f<T>(v); }
 
+// v + the value of lane l' for the DPP lane pattern CTRL (the pairing of a reduction step).
+template <int CTRL> __device__ inline float dpp_add(float v) {
+  const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true);
+  return v + __int_as_float(o);
+}
+
+// Sum over the wave, left in every lane, without LDS: DPP within each 16-lane row (quad swaps,
+// half-row mirror, row mirror), then v_permlane16_swap (lane l and l ^ 16 exchange) and
+// v_permlane32_swap (l and l ^ 32).
 __device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 __device__ inline double wave_sum_d(double v) {
 #pragma unroll
@@ -524,10 +538,6 @@ __global__ void pw_coop_kernel(int mode, const void* in, long pix, int hw, int c
 // lane group per trip so that two loads are in flight). The 6 dot products are summed across
 // the 8 lanes with DPP (the two quad swaps, then the half-row mirror), which leaves all 6 sums
 // in every lane, and the lanes share the pixel's stores.
-template <int CTRL> __device__ inline float dpp_add(float v) {
-  const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true);
-  return v + __int_as_float(o);
-}
 template <typename T>
 __global__ void __launch_bounds__(256) pw_ma128_kernel(const void* in, long pix, int hw, const float* w, const float* b,
                                                        float* o0, float* o1, float* o2, uint8_t* o3, const float* scale) {
@@ -629,7 +639,59 @@ void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, 
 }
 
 // ---------------------------------------------------------------------------------------
-// Small linears for the heads: one wave per output column n, looping over the M rows.
+// Small linears for the heads: one wave per output column n. Each lane takes 8 consecutive k
+// at a time (one 16-byte weight load) and keeps the partial sums of up to 8 rows, so the weight
+// row is read once for all rows.
+template <typename TW> __device__ inline void load_w8(const void* W, long i, float* w);
+template <> __device__ inline void load_w8<bf16>(const void* W, long i, float* w) {
+  const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(W) + i);
+  const uint32_t q[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    w[2 * k] = bf2f(bf16(q[k] & 0xffffu));
+    w[2 * k + 1] = bf2f(bf16(q[k] >> 16));
+  }
+}
+template <> __device__ inline void load_w8<float>(const void* W, long i, float* w) {
+  const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + i);
+  const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + i + 4);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
+template <typename TW>
+__global__ void small_linear8_kernel(const float* x, long ldx, int M, int K, const void* W, long ldw, const float* b,
+                                     float* y, long ldy, int N, int act) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+  if (wave >= N) return;
+  const long wb = (long)wave * ldw;
+  for (int m0 = 0; m0 < M; m0 += 8) {
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k = lane * 8; k < K; k += 512) {
+      float w[8];
+      load_w8<TW>(W, wb + k, w);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        if (m0 + m < M) {
+          const float4 a = *reinterpret_cast<const float4*>(x + long(m0 + m) * ldx + k);
+          const float4 c = *reinterpret_cast<const float4*>(x + long(m0 + m) * ldx + k + 4);
+          s[m] += w[0] * a.x + w[1] * a.y + w[2] * a.z + w[3] * a.w + w[4] * c.x + w[5] * c.y + w[6] * c.z + w[7] * c.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      if (m0 + m >= M) break;
+      const float t = wave_sum(s[m]);
+      if (lane == 0) {
+        float v = t + (b ? b[wave] : 0.f);
+        if (act == ACT_RELU) v = fmaxf(v, 0.f);
+        y[long(m0 + m) * ldy + wave] = v;
+      }
+    }
+  }
+}
+
+// Scalar form for strides or sizes the 8-wide form cannot take.
 template <typename TW>
 __global__ void small_linear_kernel(const float* x, long ldx, int M, int K, const void* W, long ldw, const float* b,
                                     float* y, long ldy, int N, int act) {
@@ -654,8 +716,15 @@ void small_linear(const Exec& ex, int wdt, const float* x, long ldx, int M, int 
   if (ex.dry || M == 0) return;
   ProfScope ps(ex, "small_linear", 2.0 * M * N * K, double(N) * K * dtype_size(wdt) + 4.0 * M * (K + N));
   dim3 grid(cdiv(N, 4));
-  if (wdt == F32) hipLaunchKernelGGL(small_linear_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
-  else hipLaunchKernelGGL(small_linear_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+  const bool vec = K % 8 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(W) & 15) == 0 && (ldw * dtype_size(wdt)) % 16 == 0;
+  if (vec) {
+    if (wdt == F32) hipLaunchKernelGGL(small_linear8_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+    else hipLaunchKernelGGL(small_linear8_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+  } else {
+    if (wdt == F32) hipLaunchKernelGGL(small_linear_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+    else hipLaunchKernelGGL(small_linear_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+  }
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -899,6 +968,43 @@ void swiglu_gate(const Exec& ex, int dt, const void* x12, int rows, int hidden, 
 
 // Block (group, 64-column chunk): the 4 waves stride over the P rows, lanes over columns,
 // then the 4 partial sums meet in LDS.
+// Mean over the P rows of each group, in two passes: blocks of (group, 512 channels, slice of
+// P/8 rows) sum 8-channel vectors into per-slice partials (4 row lanes per block, reduced in
+// LDS), then one thread per (group, channel) adds the 8 partials in order. The partials live in
+// the context workspace. A single pass (one block per 64 channels walking all P rows) took
+// 68 us at C4 for 12.7 MB.
+constexpr int MEAN_SLICES = 8;
+template <typename T>
+__global__ void __launch_bounds__(256) mean_rows_part_kernel(const void* in, int P, int C, float* part) {
+  __shared__ float red[4][64 * 8];
+  const int g = blockIdx.x, lane = threadIdx.x & 63, rl = threadIdx.x >> 6;
+  const int c = (blockIdx.y * 64 + lane) * 8;
+  const int chunk = (P + MEAN_SLICES - 1) / MEAN_SLICES, p0 = blockIdx.z * chunk, p1 = min(P, p0 + chunk);
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (c < C)
+    for (int p = p0 + rl; p < p1; p += 4) {
+      float v[8];
+      Vec8<T>::load(in, (long(g) * P + p) * C + c, v);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s[k] += v[k];
+    }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) red[rl][lane * 8 + k] = s[k];
+  __syncthreads();
+  if (rl == 0 && c < C) {
+    float* dst = part + (long(blockIdx.z) * gridDim.x + g) * C + c;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dst[k] = (red[0][lane * 8 + k] + red[1][lane * 8 + k]) + (red[2][lane * 8 + k] + red[3][lane * 8 + k]);
+  }
+}
+__global__ void mean_rows_final_kernel(const float* part, int groups, int P, int C, float* out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= groups * C) return;
+  float s = 0.f;
+  for (int r = 0; r < MEAN_SLICES; ++r) s += part[long(r) * groups * C + i];
+  out[i] = s / P;
+}
+
 template <typename T>
 __global__ void mean_rows_kernel(const void* in, int groups, int P, int C, float* out) {
   __shared__ float part[4][64];
@@ -913,8 +1019,23 @@ __global__ void mean_rows_kernel(const void* in, int groups, int P, int C, float
 }
 
 void mean_rows(const Exec& ex, int dt, const void* in, int groups, int P, int C, float* out) {
-  if (ex.dry) return;
+  const size_t pbytes = size_t(MEAN_SLICES) * groups * C * sizeof(float);
+  const bool two_pass = C % 8 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 && ex.ws;
+  if (ex.dry) {
+    if (two_pass) ex.ws->need = std::max(ex.ws->need, pbytes);
+    return;
+  }
   ProfScope ps(ex, "mean_rows", 0, double(groups) * P * C * dtype_size(dt) + 4.0 * groups * C);
+  if (two_pass && ex.ws->ptr && ex.ws->cap >= pbytes) {
+    float* part = static_cast<float*>(ex.ws->ptr);
+    dim3 grid(groups, cdiv(C / 8, 64), MEAN_SLICES);
+    if (dt == F32) hipLaunchKernelGGL(mean_rows_part_kernel<float>, grid, dim3(256), 0, ex.stream, in, P, C, part);
+    else hipLaunchKernelGGL(mean_rows_part_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, P, C, part);
+    SPLAT_HIP(hipGetLastError());
+    hipLaunchKernelGGL(mean_rows_final_kernel, dim3(cdiv(groups * C, 256)), dim3(256), 0, ex.stream, part, groups, P, C, out);
+    SPLAT_HIP(hipGetLastError());
+    return;
+  }
   dim3 grid(groups, cdiv(C, 64));
   if (dt == F32) hipLaunchKernelGGL(mean_rows_kernel<float>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
   else hipLaunchKernelGGL(mean_rows_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
