@@ -471,14 +471,19 @@ template <int N> __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt v
 
 constexpr uint32_t OOB = 0x80000000u;
 
-template <int BM, int BN, int WM, int WN, int STAGES, int BK, int AMODE, bool RELU, int EPI>
-__global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
+// T = bf16 (one v_mfma_f32_32x32x16_bf16 per k-step) or float (four v_mfma_f32_32x32x2f32):
+// a k-step is 32 bytes of K per row either way, so the tiles, loads and swizzles are the same
+// byte for byte; BK counts elements (128-byte rows: 64 bf16 or 32 fp32).
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int AMODE, bool RELU, int EPI>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32, NW = WM * WN;
-  // A tile row holds BK bf16 = RB bytes = CPR 16-byte chunks; one load instruction of a wave
-  // fills RPI rows (1 KiB). Chunk c of row r sits in slot c ^ ((r >> SH) & (CPR - 1)), which
+  constexpr int ES = sizeof(T), KE = 16 / ES;  // bytes per element, elements per 16-byte chunk
+  constexpr int MPI = ES == 4 ? 4 : 1;         // MFMA instructions per Mfma<T>::mma
+  // A tile row holds BK elements = RB bytes = CPR 16-byte chunks; one load instruction of a
+  // wave fills RPI rows (1 KiB). Chunk c of row r sits in slot c ^ ((r >> SH) & (CPR - 1)), which
   // keeps the 16 lanes of every ds_read_b128 phase on distinct banks.
-  constexpr int RB = BK * 2, CPR = RB / 16, RPI = 64 / CPR, SH = CPR == 8 ? 1 : 2, KS = BK / 16;
-  static_assert(BK == 64 || BK == 32, "k-tile");
+  constexpr int RB = BK * ES, CPR = RB / 16, RPI = 64 / CPR, SH = CPR == 8 ? 1 : 2, KS = RB / 32;
+  static_assert(RB == 128 || RB == 64, "k-tile");
   constexpr int AL = BM / (NW * RPI), BL = BN / (NW * RPI);  // load instructions per wave per k-tile
   constexpr int LPT = AL + BL;
   static_assert(AL * NW * RPI == BM && BL * NW * RPI == BN, "tile rows split evenly over the waves' loads");
@@ -513,25 +518,25 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
   // slot lane%CPR that chunk is slot ^ ((r >> SH) & (CPR-1)), the same for every i.
   const int lrow = lane / CPR;
   const int c = (lane % CPR) ^ (((wave * RPI + lrow) >> SH) & (CPR - 1));
-  const int32x4_t rw = make_rsrc(p.W, uint32_t(long(p.N) * p.ldw * 2));
+  const int32x4_t rw = make_rsrc(p.W, uint32_t(long(p.N) * p.ldw * ES));
   uint32_t boff[BL];
 #pragma unroll
   for (int i = 0; i < BL; ++i) {
     const long n = n0 + (i * NW + wave) * RPI + lrow;
-    boff[i] = n < p.N ? uint32_t(n * p.ldw * 2 + c * 16) : OOB;
+    boff[i] = n < p.N ? uint32_t(n * p.ldw * ES + c * 16) : OOB;
   }
   int32x4_t ra;
   uint32_t aoff[AL];
   int aiy[AL], aix[AL];
   if (AMODE == A_ROWS) {
-    ra = make_rsrc(p.A, uint32_t(long(p.M) * p.lda * 2));
+    ra = make_rsrc(p.A, uint32_t(long(p.M) * p.lda * ES));
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
       const long m = m0 + (i * NW + wave) * RPI + lrow;
-      aoff[i] = m < p.M ? uint32_t(m * p.lda * 2 + c * 16) : OOB;
+      aoff[i] = m < p.M ? uint32_t(m * p.lda * ES + c * 16) : OOB;
     }
   } else {
-    ra = make_rsrc(p.A, uint32_t(long(p.V) * p.Hi * p.Wi * p.Cin * 2));
+    ra = make_rsrc(p.A, uint32_t(long(p.V) * p.Hi * p.Wi * p.Cin * ES));
     const int hw = p.Ho * p.Wo;
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
@@ -541,7 +546,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
         const int oy = rem / p.Wo, ox = rem - oy * p.Wo;
         aiy[i] = oy * p.stride - p.pad;
         aix[i] = ox * p.stride - p.pad;
-        aoff[i] = uint32_t(long(v) * p.Hi * p.Wi * p.Cin * 2);
+        aoff[i] = uint32_t(long(v) * p.Hi * p.Wi * p.Cin * ES);
       } else {
         aiy[i] = -(1 << 20);
         aix[i] = 0;
@@ -559,7 +564,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
   auto issue_one = [&](int kr, int stage, int l) {
     const uint32_t sb = lds_addr(smem + stage * STAGE);
     const int kt = kt0 + kr;
-    const int k = kt * BK + c * 8;
+    const int k = kt * BK + c * KE;
     const bool kin = k < kend;
     if (l < AL) {
       const int i = l;
@@ -570,7 +575,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
         const int ky = tap / p.ks, kx = tap - ky * p.ks;
         const int iy = aiy[i] + ky, ix = aix[i] + kx;
         const bool ok = kin && iy >= 0 && iy < p.Hi && ix >= 0 && ix < p.Wi;
-        load_to_lds(ra, ok ? aoff[i] + uint32_t((iy * p.Wi + ix) * p.Cin + ci) * 2 : OOB, sb + (i * NW + wave) * 1024);
+        load_to_lds(ra, ok ? aoff[i] + uint32_t((iy * p.Wi + ix) * p.Cin + ci) * ES : OOB, sb + (i * NW + wave) * 1024);
       }
     } else {
       const int i = l - AL;
@@ -620,19 +625,19 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
       __builtin_amdgcn_sched_barrier(0);
       if (RELU) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa[s & 1][i] = Mfma<bf16>::relu(fa[s & 1][i]);
+        for (int i = 0; i < TM; ++i) fa[s & 1][i] = Mfma<T>::relu(fa[s & 1][i]);
       }
       if (s + 1 < KS || !HAS_NEXT) {
         if (s + 1 < KS) read_frags(sb, s + 1, (s + 1) & 1);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j) Mfma<bf16>::mma(acc[i][j], fa[s & 1][i], fb[s & 1][j]);
+          for (int j = 0; j < TN; ++j) Mfma<T>::mma(acc[i][j], fa[s & 1][i], fb[s & 1][j]);
         if (s + 1 < KS) {
           // interleave the LDS reads with this step's MFMAs
 #pragma unroll
           for (int k = 0; k < NF; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, MM / NF > 0 ? MM / NF : 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, MM * MPI / NF > 0 ? MM * MPI / NF : 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
           }
         }
@@ -648,7 +653,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
         const int off0 = (g ^ sw) * 16;
 #pragma unroll
         for (int q = 0; q < MM; ++q) {
-          Mfma<bf16>::mma(acc[q / TN][q % TN], fa[CUR][q / TN], fb[CUR][q % TN]);
+          Mfma<T>::mma(acc[q / TN][q % TN], fa[CUR][q / TN], fb[CUR][q % TN]);
 #pragma unroll
           for (int l = q * LPT / MM; l < (q + 1) * LPT / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l);
 #pragma unroll
@@ -667,7 +672,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_bf16_kernel(const GemmArgs 
   wait_vmcnt<0>();  // the zero-fill loads past the last tile must land before the ring is reused
   __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
   float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
-  epilogue<bf16, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
+  epilogue<T, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
                               EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr);
 }
 
@@ -693,8 +698,8 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p, in
 
 constexpr int GEMM_CUS = 256;  // MI355X compute units: one "round" of resident blocks per CU slot
 
-template <int BM, int BN, int WM, int WN, int STAGES, int BK = 64>
-static void launch_bf16(const Exec& ex, const GemmArgs& a, int S) {
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 128 / sizeof(T)>
+static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   const int tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
   const int epi = S > 1 ? EPI_PART : epi_kind(a);
   GemmArgs b = a;
@@ -705,7 +710,7 @@ static void launch_bf16(const Exec& ex, const GemmArgs& a, int S) {
   }
   dim3 grid(tm * tn * S);
 #define SPLAT_GO(AM, RL, EP) \
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(WM * WN * 64), 0, ex.stream, b, tm, tn)
+  hipLaunchKernelGGL((gemm_mfma_kernel<T, BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(WM * WN * 64), 0, ex.stream, b, tm, tn)
   if (epi == EPI_PART) {
     if (a.amode == A_ROWS) SPLAT_GO(A_ROWS, false, EPI_PART);
     else if (a.relu_in) SPLAT_GO(A_CONV, true, EPI_PART);
@@ -725,13 +730,14 @@ static void launch_bf16(const Exec& ex, const GemmArgs& a, int S) {
   SPLAT_HIP(hipGetLastError());
   if (S > 1) {
     const long work = long(a.M) * ((a.N + 7) / 8);
-    hipLaunchKernelGGL(splitk_reduce_kernel<bf16>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b, S);
+    hipLaunchKernelGGL(splitk_reduce_kernel<T>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b, S);
     SPLAT_HIP(hipGetLastError());
   }
 }
 
 // Tile configurations of the bf16 path: block tile, and how many blocks share a CU.
-enum BfCfg { CFG_128x32, CFG_128x64, CFG_256x256, CFG_256x128, CFG_320x256, CFG_320x128, CFG_192x128, CFG_128x128 };
+enum BfCfg { CFG_128x32, CFG_128x64, CFG_256x256, CFG_256x128, CFG_320x256, CFG_320x128, CFG_192x128, CFG_128x128,
+             CFG_F128x128, CFG_F64x64 };
 struct BfShape { int bm, bn, per_cu; };
 static BfShape bf_shape(BfCfg c) {
   switch (c) {
@@ -742,6 +748,8 @@ static BfShape bf_shape(BfCfg c) {
     case CFG_320x256: return {320, 256, 1};
     case CFG_320x128: return {320, 128, 1};
     case CFG_192x128: return {192, 128, 1};
+    case CFG_F128x128: return {128, 128, 2};
+    case CFG_F64x64: return {64, 64, 4};
     default: return {128, 128, 1};
   }
 }
@@ -784,7 +792,7 @@ static int split_factor(const GemmArgs& a, BfCfg c) {
   const BfShape sh = bf_shape(c);
   const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
   const long slots = long(GEMM_CUS) * sh.per_cu;
-  const int nk = cdiv(a.K, 64);
+  const int nk = cdiv(a.K, a.dt == F32 ? 32 : 64);
   if (2 * tiles > slots || nk < 16) return 1;
   const int S = int(std::min<long>(nk / 8, slots / tiles));
   if (S < 2) return 1;
@@ -794,19 +802,51 @@ static size_t split_bytes(const GemmArgs& a, int S) {
   return S > 1 ? size_t(S) * a.M * ((a.N + 7) / 8 * 8) * sizeof(float) : 0;
 }
 
+// fp32 (every GEMM of the fp32 mode): the matrix cores run fp32 at 1/16 of the bf16 rate, so
+// operand traffic is minor and the tile choice only has to fill the CUs: a round of resident
+// tiles runs per_cu tiles per CU side by side, so its cost is per_cu x the tile's area.
+static BfCfg pick_f32(const GemmArgs& a) {
+  if (a.N <= 32) return CFG_128x32;
+  if (a.N <= 64) return CFG_F64x64;
+  const BfCfg cands[] = {CFG_256x256, CFG_256x128, CFG_F128x128, CFG_F64x64};
+  double best = 1e30;
+  BfCfg pick = CFG_256x256;
+  for (BfCfg c : cands) {
+    const BfShape sh = bf_shape(c);
+    const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
+    const long slots = long(GEMM_CUS) * sh.per_cu;
+    const double cost = double((tiles + slots - 1) / slots) * sh.per_cu * sh.bm * sh.bn;
+    if (cost < best * 0.999) { best = cost; pick = c; }
+  }
+  return pick;
+}
+
+static void launch_f32_auto(const Exec& ex, const GemmArgs& a) {
+  const BfCfg c = pick_f32(a);
+  int S = split_factor(a, c);
+  if (S > 1 && !(ex.ws && ex.ws->ptr && ex.ws->cap >= split_bytes(a, S))) S = 1;
+  switch (c) {
+    case CFG_128x32: return launch_mfma<float, 128, 32, 4, 1, 2>(ex, a, S);
+    case CFG_256x256: return launch_mfma<float, 256, 256, 2, 4, 2>(ex, a, S);
+    case CFG_256x128: return launch_mfma<float, 256, 128, 4, 2, 3>(ex, a, S);
+    case CFG_F128x128: return launch_mfma<float, 128, 128, 2, 2, 2>(ex, a, S);
+    default: return launch_mfma<float, 64, 64, 2, 2, 2>(ex, a, S);
+  }
+}
+
 static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
   const BfCfg c = pick_bf16(a);
   int S = split_factor(a, c);
   if (S > 1 && !(ex.ws && ex.ws->ptr && ex.ws->cap >= split_bytes(a, S))) S = 1;
   switch (c) {
-    case CFG_128x32: return launch_bf16<128, 32, 4, 1, 2>(ex, a, S);
-    case CFG_128x64: return launch_bf16<128, 64, 2, 2, 2>(ex, a, S);
-    case CFG_256x256: return launch_bf16<256, 256, 2, 4, 2>(ex, a, S);
-    case CFG_256x128: return launch_bf16<256, 128, 4, 2, 3>(ex, a, S);
-    case CFG_320x256: return launch_bf16<320, 256, 2, 4, 2>(ex, a, S);
-    case CFG_320x128: return launch_bf16<320, 128, 2, 4, 2>(ex, a, S);
-    case CFG_192x128: return launch_bf16<192, 128, 2, 4, 3>(ex, a, S);
-    default: return launch_bf16<128, 128, 2, 2, 4>(ex, a, S);
+    case CFG_128x32: return launch_mfma<bf16, 128, 32, 4, 1, 2>(ex, a, S);
+    case CFG_128x64: return launch_mfma<bf16, 128, 64, 2, 2, 2>(ex, a, S);
+    case CFG_256x256: return launch_mfma<bf16, 256, 256, 2, 4, 2>(ex, a, S);
+    case CFG_256x128: return launch_mfma<bf16, 256, 128, 4, 2, 3>(ex, a, S);
+    case CFG_320x256: return launch_mfma<bf16, 320, 256, 2, 4, 2>(ex, a, S);
+    case CFG_320x128: return launch_mfma<bf16, 320, 128, 2, 4, 2>(ex, a, S);
+    case CFG_192x128: return launch_mfma<bf16, 192, 128, 2, 4, 3>(ex, a, S);
+    default: return launch_mfma<bf16, 128, 128, 2, 2, 4>(ex, a, S);
   }
 }
 
@@ -820,17 +860,16 @@ static void launch_cfg(const Exec& ex, const GemmArgs& a) {
   SPLAT_HIP(hipGetLastError());
 }
 
-// The MFMA bf16 path addresses its operands with 32-bit buffer offsets.
-static bool bf16_path_ok(const GemmArgs& a) {
-  const double abytes = a.amode == A_ROWS ? double(a.M) * a.lda * 2 : double(a.V) * a.Hi * a.Wi * a.Cin * 2;
-  return a.dt == BF16 && abytes < 2147483648.0 && double(a.N) * a.ldw * 2 < 2147483648.0;
+// The MFMA path addresses its operands with 32-bit buffer offsets.
+static bool mfma_path_ok(const GemmArgs& a) {
+  const double es = a.dt == F32 ? 4 : 2;
+  const double abytes = a.amode == A_ROWS ? double(a.M) * a.lda * es : double(a.V) * a.Hi * a.Wi * a.Cin * es;
+  return abytes < 2147483648.0 && double(a.N) * a.ldw * es < 2147483648.0;
 }
 
 template <typename T>
 static void launch_typed(const Exec& ex, const GemmArgs& a) {
-  if constexpr (sizeof(T) == 2) {
-    if (bf16_path_ok(a)) return launch_bf16_auto(ex, a);
-  }
+  if (mfma_path_ok(a)) return sizeof(T) == 2 ? launch_bf16_auto(ex, a) : launch_f32_auto(ex, a);
   const long tiles128 = (long)cdiv(a.M, 128) * cdiv(a.N, 128);
   if (a.N <= 32) launch_cfg<T, 256, 32, 4, 1>(ex, a);
   else if (a.N <= 64) launch_cfg<T, 256, 64, 4, 1>(ex, a);
@@ -855,8 +894,8 @@ void gemm(const Exec& ex, const GemmArgs& args) {
   if (a.store == STORE_CONVT)
     SPLAT_CHECK((long)a.ct_s * a.ct_s * a.ct_Cout == a.N && (long)a.V * a.ct_R * a.ct_C == a.M, BAD_ARGUMENT,
                 "gemm: convT geometry");
-  if (ex.dry && ex.ws && a.M > 0 && bf16_path_ok(a))  // size the split-K partials of the real run
-    ex.ws->need = std::max(ex.ws->need, split_bytes(a, split_factor(a, pick_bf16(a))));
+  if (ex.dry && ex.ws && a.M > 0 && mfma_path_ok(a))  // size the split-K partials of the real run
+    ex.ws->need = std::max(ex.ws->need, split_bytes(a, split_factor(a, a.dt == F32 ? pick_f32(a) : pick_bf16(a))));
   if (ex.dry || a.M == 0) return;
   const double es = a.dt == F32 ? 4 : 2, mn = double(a.M) * a.N;
   const double abytes = a.amode == A_ROWS ? double(a.M) * a.K * es : double(a.V) * a.Hi * a.Wi * a.Cin * es;
