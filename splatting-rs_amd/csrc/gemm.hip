@@ -19,6 +19,7 @@ namespace splat {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16> {
@@ -26,15 +27,13 @@ template <> struct Mfma<bf16> {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                   acc, 0, 0, 0);
   }
+  // max(x, 0) of bf16 pairs as signed 16-bit integers (one v_pk_max_i16 a dword): negative
+  // values, -0 included, have the sign bit set and compare below 0.
   __device__ static inline uint4 relu(uint4 v) {
     uint32_t* w = reinterpret_cast<uint32_t*>(&v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t x = w[i];
-      uint32_t lo = (x & 0x8000u) ? 0u : (x & 0xffffu);
-      uint32_t hi = (x & 0x80000000u) ? 0u : (x & 0xffff0000u);
-      w[i] = lo | hi;
-    }
+    for (int i = 0; i < 4; ++i)
+      w[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(short2_t, w[i]), short2_t{0, 0}));
     return v;
   }
 };
@@ -45,10 +44,10 @@ template <> struct Mfma<float> {
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
   }
-  __device__ static inline uint4 relu(uint4 v) {
+  __device__ static inline uint4 relu(uint4 v) {  // max(x, 0) as signed integers (v_max_i32)
     uint32_t* w = reinterpret_cast<uint32_t*>(&v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = (w[i] & 0x80000000u) ? 0u : w[i];
+    for (int i = 0; i < 4; ++i) w[i] = uint32_t(max(int(w[i]), 0));
     return v;
   }
 };
@@ -461,15 +460,23 @@ __device__ inline uint32_t lds_addr(const void* p) {
   return uint32_t(reinterpret_cast<uintptr_t>((lds_cptr)p));  // generic -> LDS address space cast
 }
 
-__device__ inline void load_to_lds(const int32x4_t& rsrc, uint32_t voffset, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(__builtin_amdgcn_readfirstlane(int(lds))),
-               "v"(voffset), "s"(rsrc)
+// 16 bytes per lane from rsrc at voffset + soffset into LDS at lds + 16 * lane. A voffset of
+// OOB (or any voffset past the buffer) reads zeros, whatever soffset holds: every valid
+// voffset + soffset stays inside the buffer, so the range check of either form (with or
+// without soffset) gives the same result.
+__device__ inline void load_to_lds(const int32x4_t& rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(__builtin_amdgcn_readfirstlane(int(lds))),
+               "v"(voffset), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(int(soffset)))
                : "memory");  // m0 is set here and used by nothing else in these kernels
 }
 
 template <int N> __device__ inline void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
 constexpr uint32_t OOB = 0x80000000u;
+
+// Kernel-side A mode of a convolution whose Cin is a multiple of the k-tile and whose filter has
+// at most 32 taps (chosen by the launcher; callers pass A_CONV): each k-tile lies in one tap.
+constexpr int A_CONV_TAP = 2;
 
 // T = bf16 (one v_mfma_f32_32x32x16_bf16 per k-step) or float (four v_mfma_f32_32x32x2f32):
 // a k-step is 32 bytes of K per row either way, so the tiles, loads and swizzles are the same
@@ -493,7 +500,8 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
   static_assert(STAGES * STAGE >= NW * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the ring");
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index is uniform: every LDS destination of the DMA loads is scalar arithmetic
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int g = lane >> 5, l32 = lane & 31;
 
@@ -528,6 +536,11 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
   int32x4_t ra;
   uint32_t aoff[AL];
   int aiy[AL], aix[AL];
+  // Convolutions whose Cin is a multiple of BK: a k-tile lies inside one filter tap, so the tap
+  // and its offset are uniform; each row keeps a bit mask of its in-bounds taps and its byte
+  // offset at tap (0, 0) (modulo 2^32: the sum with a valid tap's offset is the real offset).
+  constexpr bool conv_fast = AMODE == A_CONV_TAP;
+  uint32_t tmsk[AL], rbase[AL];
   if (AMODE == A_ROWS) {
     ra = make_rsrc(p.A, uint32_t(long(p.M) * p.lda * ES));
 #pragma unroll
@@ -552,6 +565,16 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
         aix[i] = 0;
         aoff[i] = 0;
       }
+      tmsk[i] = 0;
+      rbase[i] = 0;
+      if (conv_fast && m < p.M) {
+        rbase[i] = aoff[i] + uint32_t(((long(aiy[i]) * p.Wi + aix[i]) * p.Cin + c * KE) * ES);
+        for (int ky = 0; ky < p.ks; ++ky)
+          for (int kx = 0; kx < p.ks; ++kx) {
+            const int iy = aiy[i] + ky, ix = aix[i] + kx;
+            if (iy >= 0 && iy < p.Hi && ix >= 0 && ix < p.Wi) tmsk[i] |= 1u << (ky * p.ks + kx);
+          }
+      }
     }
   }
 
@@ -559,27 +582,44 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
   const int kt0 = split * p.kper;
   const int nk = EPI == EPI_PART ? min(nk_all - kt0, p.kper) : nk_all;
   const int kend = min(p.K, (kt0 + nk) * BK);
+  const int nk_full = (kend - kt0 * BK) / BK;  // k-tiles (from kt0) with every chunk inside [0, kend)
   // Load instruction l (l < AL: A rows, else W rows) of k-tile kt0 + kr into ring stage
-  // `stage`. K-chunks at or past kend (tail and tiles beyond the slice) read as zeros.
-  auto issue_one = [&](int kr, int stage, int l) {
+  // `stage`. K-chunks at or past kend (tail and tiles beyond the slice) read as zeros. Row
+  // operands put the k-tile offset in the scalar offset, so a load of a full k-tile (FULL:
+  // kr < nk_full, known at compile time) costs no vector instruction; rows past the operand
+  // have voffset OOB.
+  auto issue_one = [&](int kr, int stage, int l, auto full) {
+    constexpr bool FULL = decltype(full)::value;
     const uint32_t sb = lds_addr(smem + stage * STAGE);
     const int kt = kt0 + kr;
     const int k = kt * BK + c * KE;
-    const bool kin = k < kend;
+    const bool kin = FULL || k < kend;
     if (l < AL) {
       const int i = l;
       if (AMODE == A_ROWS) {
-        load_to_lds(ra, (kin && aoff[i] != OOB) ? aoff[i] + kt * RB : OOB, sb + (i * NW + wave) * 1024);
+        load_to_lds(ra, kin ? aoff[i] : OOB, uint32_t(kt) * RB, sb + (i * NW + wave) * 1024);
+      } else if constexpr (conv_fast) {
+        // uniform: tap, ci0 and the tap's offset are scalars; a row whose tap is out of bounds
+        // gets bit 31 set (every valid offset is below 2^31), a tile past kend voffset OOB
+        const int kk = kt * BK;
+        const int tap = kk / p.Cin, ci0 = kk - tap * p.Cin;
+        const int ky = tap / p.ks, kx = tap - ky * p.ks;
+        const uint32_t toff = __builtin_amdgcn_readfirstlane(int(((ky * p.Wi + kx) * p.Cin + ci0) * ES));
+        const uint32_t bad = ((tmsk[i] >> (tap & 31)) & 1u) ^ 1u;
+        uint32_t voff = (rbase[i] + toff) | (bad << 31);
+        if (!FULL && kk >= kend) voff = OOB;
+        load_to_lds(ra, voff, 0u, sb + (i * NW + wave) * 1024);
       } else {
         const int tap = k / p.Cin, ci = k - tap * p.Cin;
         const int ky = tap / p.ks, kx = tap - ky * p.ks;
         const int iy = aiy[i] + ky, ix = aix[i] + kx;
         const bool ok = kin && iy >= 0 && iy < p.Hi && ix >= 0 && ix < p.Wi;
-        load_to_lds(ra, ok ? aoff[i] + uint32_t((iy * p.Wi + ix) * p.Cin + ci) * ES : OOB, sb + (i * NW + wave) * 1024);
+        load_to_lds(ra, ok ? aoff[i] + uint32_t((iy * p.Wi + ix) * p.Cin + ci) * ES : OOB, 0u,
+                    sb + (i * NW + wave) * 1024);
       }
     } else {
       const int i = l - AL;
-      load_to_lds(rw, (kin && boff[i] != OOB) ? boff[i] + kt * RB : OOB, sb + BM * RB + (i * NW + wave) * 1024);
+      load_to_lds(rw, kin ? boff[i] : OOB, uint32_t(kt) * RB, sb + BM * RB + (i * NW + wave) * 1024);
     }
   };
 
@@ -599,24 +639,29 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
 #pragma unroll
-    for (int l = 0; l < LPT; ++l) issue_one(s, s, l);
+    for (int l = 0; l < LPT; ++l) issue_one(s, s, l, std::false_type{});
   wait_vmcnt<(STAGES - 1) * LPT>();
   __syncthreads();
   // Fragments of the next k-step (of this tile, or step 0 of the next tile) are read while the
   // matrix cores work on the current one.
   uint4 fa[2][TM], fb[2][TN];
+  // Fragment f of a k-step in the order the MFMAs (i outer, j inner) first use them: A0, then
+  // every W fragment, then A1..A(TM-1), so that the first MFMAs of a step wait for few reads.
+  auto read_frag = [&](const char* sb, int off, int slot, int f) {
+    if (f == 0) fa[slot][0] = *reinterpret_cast<const uint4*>(sb + arow0 + off);
+    else if (f <= TN) fb[slot][f - 1] = *reinterpret_cast<const uint4*>(sb + brow0 + (f - 1) * 32 * RB + off);
+    else fa[slot][f - TN] = *reinterpret_cast<const uint4*>(sb + arow0 + (f - TN) * 32 * RB + off);
+  };
   auto read_frags = [&](const char* sb, int s, int slot) {
     const int off = ((2 * s + g) ^ sw) * 16;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) fa[slot][i] = *reinterpret_cast<const uint4*>(sb + arow0 + i * 32 * RB + off);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[slot][j] = *reinterpret_cast<const uint4*>(sb + brow0 + j * 32 * RB + off);
+    for (int f = 0; f < TM + TN; ++f) read_frag(sb, off, slot, f);
   };
   read_frags(smem, 0, 0);
   // One k-tile; the last one is peeled (HAS_NEXT false) so that each step's reads and MFMAs
   // share a basic block and the LDS waits stay exact.
   constexpr int MM = TM * TN, NF = TM + TN, CUR = (KS - 1) & 1;
-  auto tile = [&](int kt, auto has_next) {
+  auto tile = [&](int kt, auto has_next, auto full) {
     constexpr bool HAS_NEXT = decltype(has_next)::value;
     const char* sb = smem + (kt % STAGES) * STAGE;
 #pragma unroll
@@ -655,20 +700,20 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
         for (int q = 0; q < MM; ++q) {
           Mfma<T>::mma(acc[q / TN][q % TN], fa[CUR][q / TN], fb[CUR][q % TN]);
 #pragma unroll
-          for (int l = q * LPT / MM; l < (q + 1) * LPT / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l);
+          for (int l = q * LPT / MM; l < (q + 1) * LPT / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l, full);
 #pragma unroll
-          for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) {
-            if (r < TM) fa[0][r] = *reinterpret_cast<const uint4*>(nb + arow0 + r * 32 * RB + off0);
-            else fb[0][r - TM] = *reinterpret_cast<const uint4*>(nb + brow0 + (r - TM) * 32 * RB + off0);
-          }
+          for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) read_frag(nb, off0, 0, r);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  for (int kt = 0; kt + 1 < nk; ++kt) tile(kt, std::true_type{});
-  tile(nk - 1, std::false_type{});
+  // tiles whose step loads tile kt + STAGES, a full one, then the rest; the last is peeled
+  int kt = 0;
+  for (; kt + 1 < nk && kt + STAGES < nk_full; ++kt) tile(kt, std::true_type{}, std::true_type{});
+  for (; kt + 1 < nk; ++kt) tile(kt, std::true_type{}, std::false_type{});
+  tile(nk - 1, std::false_type{}, std::false_type{});
   wait_vmcnt<0>();  // the zero-fill loads past the last tile must land before the ring is reused
   __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
   float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
@@ -711,19 +756,30 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   dim3 grid(tm * tn * S);
 #define SPLAT_GO(AM, RL, EP) \
   hipLaunchKernelGGL((gemm_mfma_kernel<T, BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(WM * WN * 64), 0, ex.stream, b, tm, tn)
-  if (epi == EPI_PART) {
-    if (a.amode == A_ROWS) SPLAT_GO(A_ROWS, false, EPI_PART);
-    else if (a.relu_in) SPLAT_GO(A_CONV, true, EPI_PART);
-    else SPLAT_GO(A_CONV, false, EPI_PART);
-  } else if (a.amode == A_ROWS) {
-    if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
+  // Convolutions take the per-tap path (A_CONV_TAP) when Cin is a multiple of the k-tile, else
+  // the per-lane im2col arithmetic (A_CONV, without ReLU-on-load: no such caller).
+  const bool tap = a.amode == A_CONV && a.Cin % BK == 0 && a.ks * a.ks <= 32;
+  SPLAT_CHECK(a.amode == A_ROWS || tap || !a.relu_in, BAD_ARGUMENT,
+              "gemm: ReLU-on-load needs a convolution whose Cin is a multiple of the k-tile");
+  if (a.amode == A_ROWS) {
+    if (epi == EPI_PART) SPLAT_GO(A_ROWS, false, EPI_PART);
+    else if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
     else if (epi == EPI_RES) SPLAT_GO(A_ROWS, false, EPI_RES);
     else SPLAT_GO(A_ROWS, false, EPI_FULL);
-  } else if (epi == EPI_BIAS) {
-    if (a.relu_in) SPLAT_GO(A_CONV, true, EPI_BIAS);
-    else SPLAT_GO(A_CONV, false, EPI_BIAS);
+  } else if (tap) {
+    if (epi == EPI_PART) {
+      if (a.relu_in) SPLAT_GO(A_CONV_TAP, true, EPI_PART);
+      else SPLAT_GO(A_CONV_TAP, false, EPI_PART);
+    } else if (epi == EPI_BIAS) {
+      if (a.relu_in) SPLAT_GO(A_CONV_TAP, true, EPI_BIAS);
+      else SPLAT_GO(A_CONV_TAP, false, EPI_BIAS);
+    } else {
+      if (a.relu_in) SPLAT_GO(A_CONV_TAP, true, EPI_FULL);
+      else SPLAT_GO(A_CONV_TAP, false, EPI_FULL);
+    }
   } else {
-    if (a.relu_in) SPLAT_GO(A_CONV, true, EPI_FULL);
+    if (epi == EPI_PART) SPLAT_GO(A_CONV, false, EPI_PART);
+    else if (epi == EPI_BIAS) SPLAT_GO(A_CONV, false, EPI_BIAS);
     else SPLAT_GO(A_CONV, false, EPI_FULL);
   }
 #undef SPLAT_GO
