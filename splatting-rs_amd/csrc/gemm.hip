@@ -633,14 +633,21 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
 
   const int sw = (l32 >> SH) & (CPR - 1);  // fragment rows are l32 plus multiples of 32
   const int arow0 = (wm * (BM / WM) + l32) * RB, brow0 = (BM + wn * (BN / WN) + l32) * RB;
-  // Prologue: STAGES tiles in flight, tile 0 resident for every wave, its first fragments read.
+  // Prologue: AHEAD tiles in flight, tile 0 resident for every wave, its first fragments read.
   // Every k-tile slot is loaded, also past the last tile (as zeros), so that the number of
   // loads in flight, and with it each vmcnt wait, is the same for every tile.
+  // With three or more stages (SPREAD) tile kt issues the loads of tile kt + STAGES - 1 during
+  // its steps before the barrier step, into the stage that tile kt - 1 left: a DMA load holds
+  // up the wave that issues it, so loads crowded into one step leave the matrix core idle (the
+  // 6222x1024x4096 GEMM on 256x128 tiles: 61 -> 52 us). With two stages a stage frees only at
+  // the barrier, and the loads of tile kt + 2 go into the barrier step.
+  constexpr bool SPREAD = STAGES >= 3;
+  constexpr int AHEAD = SPREAD ? STAGES - 1 : STAGES;  // tile kt loads tile kt + AHEAD
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s)
+  for (int s = 0; s < AHEAD; ++s)
 #pragma unroll
     for (int l = 0; l < LPT; ++l) issue_one(s, s, l, std::false_type{});
-  wait_vmcnt<(STAGES - 1) * LPT>();
+  wait_vmcnt<(AHEAD - 1) * LPT>();
   __syncthreads();
   // Fragments of the next k-step (of this tile, or step 0 of the next tile) are read while the
   // matrix cores work on the current one.
@@ -672,7 +679,22 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
 #pragma unroll
         for (int i = 0; i < TM; ++i) fa[s & 1][i] = Mfma<T>::relu(fa[s & 1][i]);
       }
-      if (s + 1 < KS || !HAS_NEXT) {
+      if (SPREAD && s + 1 < KS) {
+        // this step's share of the loads of tile kt + AHEAD and the reads of the next step's
+        // fragments, spread between the MFMAs
+        const int L0 = s * LPT / (KS - 1), L1 = (s + 1) * LPT / (KS - 1);
+        const int off = ((2 * (s + 1) + g) ^ sw) * 16;
+#pragma unroll
+        for (int q = 0; q < MM; ++q) {
+          Mfma<T>::mma(acc[q / TN][q % TN], fa[s & 1][q / TN], fb[s & 1][q % TN]);
+#pragma unroll
+          for (int l = L0 + q * (L1 - L0) / MM; l < L0 + (q + 1) * (L1 - L0) / MM; ++l)
+            issue_one(kt + AHEAD, (kt + AHEAD) % STAGES, l, full);
+#pragma unroll
+          for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) read_frag(sb, off, (s + 1) & 1, r);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else if (s + 1 < KS || !HAS_NEXT) {
         if (s + 1 < KS) read_frags(sb, s + 1, (s + 1) & 1);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -688,10 +710,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
         }
       } else {
         // Last step of a tile with a successor. Every wave holds its last fragments of tile kt
-        // (the barrier waits for LDS reads), so the stage of tile kt takes tile kt+STAGES, once
-        // tile kt+1 is resident. The loads of tile kt+STAGES and the reads of the next tile's
-        // first fragments are spread between this step's MFMAs, in a fixed order, so that the
-        // load queue never fills up in front of the matrix core.
+        // (the barrier waits for LDS reads), so the stage of tile kt is free once tile kt+1 is
+        // resident (tiles kt+2 .. kt+STAGES-1 may still be in flight). With two stages the
+        // loads of tile kt+2 and the reads of the next tile's first fragments are spread
+        // between this step's MFMAs, in a fixed order; with more, only the reads.
         wait_vmcnt<(STAGES - 2) * LPT>();
         __syncthreads();
         const char* nb = smem + ((kt + 1) % STAGES) * STAGE;
@@ -699,8 +721,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
 #pragma unroll
         for (int q = 0; q < MM; ++q) {
           Mfma<T>::mma(acc[q / TN][q % TN], fa[CUR][q / TN], fb[CUR][q % TN]);
+          if constexpr (!SPREAD) {
 #pragma unroll
-          for (int l = q * LPT / MM; l < (q + 1) * LPT / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l, full);
+            for (int l = q * LPT / MM; l < (q + 1) * LPT / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l, full);
+          }
 #pragma unroll
           for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) read_frag(nb, off0, 0, r);
           __builtin_amdgcn_sched_barrier(0);
@@ -709,9 +733,9 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // tiles whose step loads tile kt + STAGES, a full one, then the rest; the last is peeled
+  // tiles whose loads are of a full tile (kt + AHEAD), then the rest; the last is peeled
   int kt = 0;
-  for (; kt + 1 < nk && kt + STAGES < nk_full; ++kt) tile(kt, std::true_type{}, std::true_type{});
+  for (; kt + 1 < nk && kt + AHEAD < nk_full; ++kt) tile(kt, std::true_type{}, std::true_type{});
   for (; kt + 1 < nk; ++kt) tile(kt, std::true_type{}, std::false_type{});
   tile(nk - 1, std::false_type{}, std::false_type{});
   wait_vmcnt<0>();  // the zero-fill loads past the last tile must land before the ring is reused
