@@ -11,6 +11,8 @@
 // row max needs one exchange between lanes l and l^32.
 #include "kernels.h"
 
+#include <type_traits>
+
 namespace splat {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -371,7 +373,8 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
   }
   const int sw = (l32 >> 1) & 7;
 
-  auto tile = [&](int t, int kbuf, int vbuf, bool masked) {
+  auto tile = [&](int t, int kbuf, int vbuf, auto masked_t) {
+    constexpr bool masked = decltype(masked_t)::value;
     const char* kb = smem + kbuf * KBYTES;
     const char* vt = smem + (2 + vbuf) * KBYTES;
     f32x16 s[QT][2];
@@ -387,7 +390,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
                                                                __builtin_bit_cast(bf16x8_t, qf[qt][st]),
                                                                st == 0 ? zero : s[qt][kt2], 0, 0, 0);
       }
-    if (masked) {  // last tile only: one code path keeps O in the same registers every tile
+    if constexpr (masked) {  // the peeled last tile only
       const int k0 = t * 64;
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt)
@@ -463,14 +466,17 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
   issue_v(0, 0);
   wait_vm<0>();
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
+  // Every tile but the last runs without the key mask (a runtime flag inside one loop body was
+  // turned into selects that ran on every tile: ~100 VALU instructions per 64-key tile).
+  for (int t = 0; t + 1 < ntiles; ++t) {
     // buffers (t+1)&1 held tile t-1, which every wave finished before the last barrier
     issue_k(t + 1, (t + 1) & 1);
     issue_v(t + 1, (t + 1) & 1);
-    tile(t, t & 1, t & 1, t + 1 == ntiles);
-    wait_vm<0>();  // this wave's share of tile t+1 (zero-fill loads past the last tile included)
+    tile(t, t & 1, t & 1, std::false_type{});
+    wait_vm<0>();  // this wave's share of tile t+1
     __syncthreads();
   }
+  tile(ntiles - 1, (ntiles - 1) & 1, (ntiles - 1) & 1, std::true_type{});
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
