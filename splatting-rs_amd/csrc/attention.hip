@@ -11,11 +11,14 @@
 // row max needs one exchange between lanes l and l^32.
 #include "kernels.h"
 
+#include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 namespace splat {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace {
@@ -277,7 +280,9 @@ template <int N> __device__ inline void wait_vm() { asm volatile("s_waitcnt vmcn
 
 }  // namespace
 
-template <int WAVES, int QT>
+// SPLIT: the block covers key tiles [split * tps, (split + 1) * tps) of its sequence and writes
+// its unnormalised O and (max, sum) to p.part; attn_combine_kernel merges the slices.
+template <int WAVES, int QT, bool SPLIT>
 __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs p, float c) {
   constexpr int KBYTES = 64 * 128;            // K or V tile: 64 keys x 128 bytes, swizzled, unpadded
   constexpr int KL = 8 / WAVES;               // load instructions per wave per K (or V) tile
@@ -292,9 +297,12 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
   const int L = p.L;
   // 1D grid over (query block, head, sequence), query blocks fastest; the query blocks of one
   // head, which all stream the same K and V, run on one XCD.
+  // (query block, slice) fastest, so that the blocks streaming one slice of one head's K and V
+  // run on one XCD
   const int nq = (L + WAVES * QT * 32 - 1) / (WAVES * QT * 32);
-  const int id = xcd_contiguous(blockIdx.x, nq * p.heads * p.seqs);
-  const int qb = id % nq, h = (id / nq) % p.heads, sq = id / (nq * p.heads);
+  const int ns = SPLIT ? p.nsplit : 1;
+  const int id = xcd_contiguous(blockIdx.x, nq * ns * p.heads * p.seqs);
+  const int qb = id % nq, split = (id / nq) % ns, h = (id / (nq * ns)) % p.heads, sq = id / (nq * ns * p.heads);
   const long base = long(sq) * p.seq_stride;
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + h * 64;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + h * 64;
@@ -428,18 +436,11 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
       }
     }
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      float ps = 0.f;
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
       for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(s[qt][kt2][r], c, -mref[qt]));
-          s[qt][kt2][r] = e;
-          ps += e;
-        }
-      lsum[qt] += ps;
-    }
+        for (int r = 0; r < 16; ++r) s[qt][kt2][r] = __builtin_amdgcn_exp2f(fmaf(s[qt][kt2][r], c, -mref[qt]));
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
 #pragma unroll
@@ -456,33 +457,62 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
               pw[i] = pack_bf16x2(s[qt][kt2][8 * hh + 2 * i], s[qt][kt2][8 * hh + 2 * i + 1]);
             o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf),
                                                                 __builtin_bit_cast(bf16x8_t, pf), o[qt][dt], 0, 0, 0);
+            if (dt == 0) {  // the running sum of the bf16 P the matrix cores use: one dot2 per pair
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                lsum[qt] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw[i]),
+                                                           __builtin_bit_cast(bf16x2_t, 0x3f803f80u), lsum[qt], false);
+            }
           }
         }
     }
   };
 
   const int ntiles = (L + 63) / 64;
-  issue_k(0, 0);
-  issue_v(0, 0);
+  const int t0 = SPLIT ? split * p.tps : 0, t1 = SPLIT ? min(ntiles, t0 + p.tps) : ntiles;
+  issue_k(t0, 0);
+  issue_v(t0, 0);
   wait_vm<0>();
   __syncthreads();
   // Every tile but the last runs without the key mask (a runtime flag inside one loop body was
   // turned into selects that ran on every tile: ~100 VALU instructions per 64-key tile).
-  for (int t = 0; t + 1 < ntiles; ++t) {
+  for (int t = t0; t + 1 < t1; ++t) {
     // buffers (t+1)&1 held tile t-1, which every wave finished before the last barrier
-    issue_k(t + 1, (t + 1) & 1);
-    issue_v(t + 1, (t + 1) & 1);
-    tile(t, t & 1, t & 1, std::false_type{});
+    const int b = (t - t0) & 1;
+    issue_k(t + 1, b ^ 1);
+    issue_v(t + 1, b ^ 1);
+    tile(t, b, b, std::false_type{});
     wait_vm<0>();  // this wave's share of tile t+1
     __syncthreads();
   }
-  tile(ntiles - 1, (ntiles - 1) & 1, (ntiles - 1) & 1, std::true_type{});
+  // the slice's last tile, with the key mask (a no-op unless it holds the sequence's ragged
+  // end): one peeled copy, as a second one (unmasked) cost 50 more VGPRs and half the occupancy
+  const int bl = (t1 - 1 - t0) & 1;
+  tile(t1 - 1, bl, bl, std::true_type{});
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const auto l2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum[qt]), __float_as_uint(lsum[qt]), false, false);
-    const float inv = 1.f / (__uint_as_float(l2[0]) + __uint_as_float(l2[1]));
+    const float tot = __uint_as_float(l2[0]) + __uint_as_float(l2[1]);
     const int qrow = q0 + qt * 32 + l32;
+    if constexpr (SPLIT) {
+      if (qrow < L) {
+        const long row = long(sq) * L + qrow, rows = long(p.seqs) * L;  // dense slice rows
+        float* O = p.part + (long(split) * rows + row) * (long(p.heads) * 64) + h * 64;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            *reinterpret_cast<float4*>(O + dt * 32 + 8 * q4 + 4 * g) =
+                make_float4(o[qt][dt][4 * q4], o[qt][dt][4 * q4 + 1], o[qt][dt][4 * q4 + 2], o[qt][dt][4 * q4 + 3]);
+        if (g == 0) {
+          float* ml = p.part + long(p.nsplit) * rows * p.heads * 64 + ((long(split) * rows + row) * p.heads + h) * 2;
+          *reinterpret_cast<float2*>(ml) = make_float2(mref[qt], tot);
+        }
+      }
+      continue;
+    }
+    const float inv = 1.f / tot;
     if (qrow < L) {
       bf16* O = reinterpret_cast<bf16*>(p.o) + (base + qrow) * p.ldo + h * 64;
 #pragma unroll
@@ -498,11 +528,80 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
   }
 }
 
+// Merges the key slices of a split launch: per query and head, M = max of the slices' maxima,
+// O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (the maxima are in exp2 units). One thread
+// per 8 head channels.
+__global__ void __launch_bounds__(256) attn_combine_kernel(const AttnArgs p) {
+  const long rows = long(p.seqs) * p.L;
+  const long id = long(blockIdx.x) * 256 + threadIdx.x;
+  if (id >= rows * p.heads * 8) return;
+  const long row = id / (p.heads * 8);
+  const int rem = int(id - row * p.heads * 8), h = rem >> 3, c8 = (rem & 7) * 8;
+  const long so = rows * p.heads * 64;
+  const float* ml = p.part + long(p.nsplit) * so;
+  float mx = -INFINITY;
+  for (int s = 0; s < p.nsplit; ++s) mx = fmaxf(mx, ml[((s * rows + row) * p.heads + h) * 2]);
+  float acc[8] = {}, den = 0.f;
+  for (int s = 0; s < p.nsplit; ++s) {
+    const float2 m_l = *reinterpret_cast<const float2*>(ml + ((s * rows + row) * p.heads + h) * 2);
+    const float w = __builtin_amdgcn_exp2f(m_l.x - mx);
+    den += w * m_l.y;
+    const float* src = p.part + s * so + row * p.heads * 64 + h * 64 + c8;
+    const float4 a = *reinterpret_cast<const float4*>(src), b = *reinterpret_cast<const float4*>(src + 4);
+    acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
+    acc[4] += w * b.x; acc[5] += w * b.y; acc[6] += w * b.z; acc[7] += w * b.w;
+  }
+  const float inv = 1.f / den;
+  uint4 u;
+  u.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+  u.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  u.z = pack_bf16x2(acc[4] * inv, acc[5] * inv);
+  u.w = pack_bf16x2(acc[6] * inv, acc[7] * inv);
+  const long seq = row / p.L, t = row - seq * p.L;
+  *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p.o) + (seq * p.seq_stride + t) * p.ldo + h * 64 + c8) = u;
+}
+
+// Key slices for a long-sequence bf16 launch whose grid would leave the last round of block
+// slots mostly empty: S minimises ceil(blocks * S / CUs) / S, the per-CU rounds of 1/S-size
+// blocks, plus 2% per slice for the partials and the merge, over S = 1..4 with at least 8 key
+// tiles a slice (C4 global 196 -> 172 us with 3 slices, C5 global 2207 -> 2092 us with 3,
+// DA3-Small C2 global 122 -> 85 us with 4).
+static int attn_splits(long blocks, int ntiles) {
+  int best = 1;
+  double bc = 1e30;
+  for (int S = 1; S <= 4; ++S) {
+    if (S > 1 && ntiles / S < 8) break;
+    const double per_cu = std::ceil(double(blocks) * S / 256.0);
+    const double cost = per_cu / S * (1.0 + (S > 1 ? 0.02 * S : 0.0));
+    if (cost < bc * 0.999) { bc = cost; best = S; }
+  }
+  return best;
+}
+
 void attention(const Exec& ex, const AttnArgs& a) {
   const int ke = a.dt == F32 ? 4 : 8;
   SPLAT_CHECK(a.L > 0 && a.heads > 0 && a.seqs > 0, BAD_ARGUMENT, "attention: bad sizes");
   SPLAT_CHECK(a.ld % ke == 0 && a.ldo % 4 == 0 && a.ld >= (long)a.heads * 64, BAD_ARGUMENT, "attention: strides");
   SPLAT_CHECK(a.seqs == 1 || a.seq_stride >= a.L, BAD_ARGUMENT, "attention: overlapping sequences");
+  const bool bf_fast = a.dt != F32 && long(a.L) * a.ld * 2 < 2147483648L && a.ld % 8 == 0 && a.ldo % 4 == 0;
+  // 4 waves x 32 or 64 queries. Two query sub-tiles per wave (QT = 2) halve the K/V reads per
+  // query and win once their grid still gives each CU about two blocks (C5 global 2.46 vs
+  // 2.85 ms, C4 encoder 56 vs 62 us); below that the doubled block size leaves CUs idle
+  // (C4 global 261 vs 242 us).
+  const long blocks2 = long(cdiv(a.L, 256)) * a.heads * a.seqs;
+  const bool qt2 = blocks2 >= 450;
+  const long blocks = qt2 ? blocks2 : long(cdiv(a.L, 128)) * a.heads * a.seqs;
+  const int ntiles = cdiv(a.L, 64);
+  const int S = bf_fast && a.L >= 4096 ? attn_splits(blocks, ntiles) : 1;
+  AttnArgs b = a;
+  if (S > 1) {
+    b.tps = cdiv(ntiles, S);
+    b.nsplit = cdiv(ntiles, b.tps);  // every slice non-empty
+    const size_t need = size_t(b.nsplit) * a.seqs * a.L * a.heads * (64 + 2) * sizeof(float);
+    if (ex.dry && ex.ws) ex.ws->need = std::max(ex.ws->need, need);
+    if (!ex.dry && !(ex.ws && ex.ws->ptr && ex.ws->cap >= need)) b.nsplit = 1;  // not sized: one slice
+    b.part = b.nsplit > 1 ? static_cast<float*>(ex.ws->ptr) : nullptr;
+  }
   if (ex.dry) return;
   const double rows = double(a.seqs) * a.L * a.heads;
   ProfScope ps(ex, "attention", 4.0 * rows * a.L * 64, 4.0 * rows * 64 * (a.dt == F32 ? 4 : 2));
@@ -510,16 +609,19 @@ void attention(const Exec& ex, const AttnArgs& a) {
   if (a.dt == F32) {
     dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
     hipLaunchKernelGGL(attn_kernel<float>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);
-  } else if (long(a.L) * a.ld * 2 < 2147483648L && a.ld % 8 == 0 && a.ldo % 4 == 0) {
-    // 4 waves x 32 or 64 queries. Two query sub-tiles per wave (QT = 2) halve the K/V reads per
-    // query and win once their grid still gives each CU about two blocks (C5 global 2.46 vs
-    // 2.85 ms, C4 encoder 56 vs 62 us); below that the doubled block size leaves CUs idle
-    // (C4 global 261 vs 242 us).
-    const long blocks2 = long(cdiv(a.L, 256)) * a.heads * a.seqs;
-    if (blocks2 >= 450)
-      hipLaunchKernelGGL((attn_bf16_kernel<4, 2>), dim3(blocks2), dim3(256), 0, ex.stream, a, c);
-    else
-      hipLaunchKernelGGL((attn_bf16_kernel<4, 1>), dim3(cdiv(a.L, 128) * a.heads * a.seqs), dim3(256), 0, ex.stream, a, c);
+  } else if (bf_fast) {
+    const dim3 grid(unsigned(blocks * b.nsplit));
+    if (b.nsplit > 1) {
+      if (qt2) hipLaunchKernelGGL((attn_bf16_kernel<4, 2, true>), grid, dim3(256), 0, ex.stream, b, c);
+      else hipLaunchKernelGGL((attn_bf16_kernel<4, 1, true>), grid, dim3(256), 0, ex.stream, b, c);
+      SPLAT_HIP(hipGetLastError());
+      const long work = long(a.seqs) * a.L * a.heads * 8;
+      hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b);
+    } else if (qt2) {
+      hipLaunchKernelGGL((attn_bf16_kernel<4, 2, false>), grid, dim3(256), 0, ex.stream, b, c);
+    } else {
+      hipLaunchKernelGGL((attn_bf16_kernel<4, 1, false>), grid, dim3(256), 0, ex.stream, b, c);
+    }
   } else {
     dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
     hipLaunchKernelGGL(attn_kernel<bf16>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);

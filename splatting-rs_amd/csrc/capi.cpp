@@ -363,7 +363,12 @@ int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out
     a.heads = heads;
     a.seqs = S;
     a.seq_stride = L;
-    attention(C(ctx)->ex, a);
+    Context* c = C(ctx);
+    Exec dry = c->ex;  // a dry pass sizes the key-split partials first
+    dry.dry = true;
+    attention(dry, a);
+    if (c->reserve_workspace()) c->clear_graphs();
+    attention(c->ex, a);
   });
 }
 

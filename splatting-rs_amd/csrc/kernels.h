@@ -57,6 +57,10 @@ struct AttnArgs {
   const void* q = nullptr; const void* k = nullptr; const void* v = nullptr; long ld = 0;
   void* o = nullptr; long ldo = 0;
   int L = 0, heads = 0, seqs = 1; long seq_stride = 0;
+  // Set by attention() for a key-split launch: nsplit slices of tps 64-key tiles each; part
+  // holds the unnormalised fp32 O of every slice, [nsplit][seqs*L][heads*64], then each
+  // slice's (max, sum) per query and head, [nsplit][seqs*L][heads][2].
+  int nsplit = 1, tps = 0; float* part = nullptr;
 };
 void attention(const Exec& ex, const AttnArgs& a);
 

@@ -106,6 +106,9 @@ ATTN_CASES = [
     (2, 1037, 16),
     (6, 1037, 16),   # two query sub-tiles per wave (large grid)
     (8, 1100, 12),   # the same with a ragged last key tile
+    # long sequences whose grid leaves block slots idle: key slices merged by a second kernel
+    (1, 6223, 12),   # the MapAnything C4 global block (3 slices, ragged last tile)
+    (1, 4096, 33),   # two query sub-tiles per wave with slices, no ragged tile
 ]
 
 
