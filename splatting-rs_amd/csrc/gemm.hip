@@ -162,7 +162,7 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
 // multiply every optional feature, and instruction fetch, not memory, then bounds the
 // epilogue):
 //   EPI_BIAS  out = act(acc + bias)                          row-major, 16-byte runs
-//   EPI_RES   out = act(acc + bias) * gamma + res            row-major, 16-byte runs
+//   EPI_RES   out = act(acc + bias) * gamma + res (+ res2)   row-major, 16-byte runs
 //   EPI_FULL  every feature (table add, row remap, second residual, transposed-conv
 //             scatter, unaligned or ragged runs) through epi8.
 // In the first two a lane always owns the same column run (RUNS divides 64), so bias and
@@ -247,7 +247,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
     for (int k = 0; k < 8; ++k) { cb[k] = 0.f; cg[k] = 1.f; }
     if (nok && p.bias) load8(p.bias, n, true, cb);
     if (EPI == EPI_RES && nok && p.gamma) load8(p.gamma, n, true, cg);
-    const bool rf = p.res_f32 || sizeof(T) == 4;
+    const bool rf = p.res_f32 || sizeof(T) == 4, rf2 = p.res2_f32 || sizeof(T) == 4;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       stage_slab<TM, TN>(acc, i, slab, lane);
@@ -260,6 +260,18 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
           const long m = wrow0 + i * 32 + rr;
           read8(slab + rr * LD + cc, v[t]);
           if (EPI == EPI_RES && p.res && nok && m < p.M) load8(p.res, m * p.ldres + n, rf, rv[t]);
+        }
+        if (EPI == EPI_RES && p.res2) {  // second residual (the DPT residual units' skip input)
+#pragma unroll
+          for (int t = 0; t < CH; ++t) {
+            const long m = wrow0 + i * 32 + rsub + (t0 + t) * (64 / RUNS);
+            float r2[8];
+            if (nok && m < p.M) {
+              load8(p.res2, m * p.ldres2 + n, rf2, r2);
+#pragma unroll
+              for (int k = 0; k < 8; ++k) rv[t][k] += r2[k];
+            }
+          }
         }
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
@@ -292,7 +304,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
 
 // Which epilogue variant a launch needs (host side; `a.epi_vec` already set).
 inline int epi_kind(const GemmArgs& a) {
-  if (!a.epi_vec || a.rm_P || a.store != STORE_ROWS || a.addtab || a.res2 || a.act_post) return EPI_FULL;
+  if (!a.epi_vec || a.rm_P || a.store != STORE_ROWS || a.addtab || a.act_post || (a.res2 && !a.res)) return EPI_FULL;
   return (a.res || a.gamma) ? EPI_RES : EPI_BIAS;
 }
 
@@ -797,6 +809,8 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
     } else if (epi == EPI_BIAS) {
       if (a.relu_in) SPLAT_GO(A_CONV_TAP, true, EPI_BIAS);
       else SPLAT_GO(A_CONV_TAP, false, EPI_BIAS);
+    } else if (epi == EPI_RES && !a.relu_in) {  // the residual units' second conv
+      SPLAT_GO(A_CONV_TAP, false, EPI_RES);
     } else {
       if (a.relu_in) SPLAT_GO(A_CONV_TAP, true, EPI_FULL);
       else SPLAT_GO(A_CONV_TAP, false, EPI_FULL);

@@ -373,9 +373,12 @@ void fusion_block(Context& ctx, int dt, const FusionW& f, const void* x, const v
   g4.res = xs;
   g4.ldres = F;
   gemm(ex, g4);
-  void* up = ctx.arena.alloc(size_t(V) * oh * ow * F * dtype_size(dt));
-  resize_bilinear(ex, dt, y, V, h, w, F, up, oh_full, ow_full, oh, ow, nullptr, 0);
-  gemm(ex, lin_args(f.out, dt, up, F, V * oh * ow, out, F));
+  // out_conv (1x1) before the bilinear resize instead of after: the resize's weights per output
+  // pixel sum to 1, so the two commute exactly (bias included) and the 1x1 runs on a quarter
+  // of the pixels
+  void* z = ctx.arena.alloc(bytes);
+  gemm(ex, lin_args(f.out, dt, y, F, V * h * w, z, F));
+  resize_bilinear(ex, dt, z, V, h, w, F, out, oh_full, ow_full, oh, ow, nullptr, 0);
   ctx.arena.release(mark);
 }
 

@@ -139,7 +139,8 @@ GemmArgs lin_args(const Lin& l, int dt, const void* in, long lda, int rows, void
 
 // DPT fusion block (depthanything3-rs/src/dpt.rs:130-137, mapanything-rs/src/dpt.rs:235-242):
 // out_conv(resize(RCU2(x + RCU1(skip)))) with RCU(x) = conv2(relu(conv1(relu(x)))) + x; the
-// resize samples an (oh_full, ow_full) grid and keeps its first (oh, ow).
+// resize samples an (oh_full, ow_full) grid and keeps its first (oh, ow). Computed as
+// resize(out_conv(...)): the 1x1 conv commutes with a bilinear resize.
 struct RcuW { Conv c1, c2; };
 struct FusionW { bool skip = false; RcuW u1, u2; Lin out; };
 void fusion_block(Context& ctx, int dt, const FusionW& f, const void* x, const void* skip, int V, int h, int w,
