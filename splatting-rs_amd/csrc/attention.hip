@@ -79,7 +79,9 @@ template <> struct AttnOps<float> {
 
 constexpr int ATTN_WAVES = 4;
 
-template <typename T>
+// SPLIT: the block covers key tiles [split * tps, (split + 1) * tps) and writes its unnormalised
+// O and (max, sum) to p.part for attn_combine_kernel, as the bf16 kernel below does.
+template <typename T, bool SPLIT>
 __global__ void __launch_bounds__(ATTN_WAVES * 64) attn_kernel(const AttnArgs p, float c) {
   constexpr int ES = sizeof(T);
   constexpr int KE = 16 / ES;              // elements per 16-byte fragment
@@ -96,7 +98,9 @@ __global__ void __launch_bounds__(ATTN_WAVES * 64) attn_kernel(const AttnArgs p,
   const int g = lane >> 5, l32 = lane & 31;
   const int h = blockIdx.y;
   const long base = (long)blockIdx.z * p.seq_stride;
-  const long q0 = (long)blockIdx.x * (ATTN_WAVES * 32) + wave * 32;
+  const int nq = (p.L + ATTN_WAVES * 32 - 1) / (ATTN_WAVES * 32);
+  const int qb = SPLIT ? int(blockIdx.x) % nq : int(blockIdx.x), split = SPLIT ? int(blockIdx.x) / nq : 0;
+  const long q0 = (long)qb * (ATTN_WAVES * 32) + wave * 32;
   const T* Q = reinterpret_cast<const T*>(p.q) + h * 64;
   const T* K = reinterpret_cast<const T*>(p.k) + h * 64;
   const T* V = reinterpret_cast<const T*>(p.v) + h * 64;
@@ -172,12 +176,13 @@ __global__ void __launch_bounds__(ATTN_WAVES * 64) attn_kernel(const AttnArgs p,
   float m = -INFINITY, lsum = 0.f;
 
   const int ntiles = (p.L + 63) / 64;
-  gload(0);
+  const int t0 = SPLIT ? split * p.tps : 0, t1 = SPLIT ? min(ntiles, t0 + p.tps) : ntiles;
+  gload(t0);
   sstore(0);
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
+  for (int t = t0; t < t1; ++t) {
+    const int buf = (t - t0) & 1;
+    if (t + 1 < t1) gload(t + 1);
     f32x16 s[2];
 #pragma unroll
     for (int kt2 = 0; kt2 < 2; ++kt2) {
@@ -223,11 +228,28 @@ __global__ void __launch_bounds__(ATTN_WAVES * 64) attn_kernel(const AttnArgs p,
 #pragma unroll
       for (int kt2 = 0; kt2 < 2; ++kt2) AttnOps<T>::pv(o[dt], vrow, kt2, g, s[kt2]);
     }
-    if (t + 1 < ntiles) sstore(buf ^ 1);
+    if (t + 1 < t1) sstore(buf ^ 1);
     __syncthreads();
   }
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
+  if constexpr (SPLIT) {
+    if (qok) {
+      const long rows = long(p.seqs) * p.L, row = long(blockIdx.z) * p.L + qrow;  // dense slice rows
+      float* O = p.part + (long(split) * rows + row) * (long(p.heads) * 64) + h * 64;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          *reinterpret_cast<float4*>(O + dt * 32 + 8 * q4 + 4 * g) =
+              make_float4(o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+      if (g == 0) {  // the max in exp2 units, as the merge expects
+        float* ml = p.part + long(p.nsplit) * rows * p.heads * 64 + ((long(split) * rows + row) * p.heads + h) * 2;
+        *reinterpret_cast<float2*>(ml) = make_float2(m * c, ltot);
+      }
+    }
+    return;
+  }
   const float inv = 1.f / ltot;
   if (qok) {
     T* O = reinterpret_cast<T*>(p.o) + (base + qrow) * p.ldo + h * 64;
@@ -531,6 +553,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
 // Merges the key slices of a split launch: per query and head, M = max of the slices' maxima,
 // O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (the maxima are in exp2 units). One thread
 // per 8 head channels.
+template <typename T>
 __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnArgs p) {
   const long rows = long(p.seqs) * p.L;
   const long id = long(blockIdx.x) * 256 + threadIdx.x;
@@ -552,13 +575,13 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnArgs p) {
     acc[4] += w * b.x; acc[5] += w * b.y; acc[6] += w * b.z; acc[7] += w * b.w;
   }
   const float inv = 1.f / den;
-  uint4 u;
-  u.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
-  u.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
-  u.z = pack_bf16x2(acc[4] * inv, acc[5] * inv);
-  u.w = pack_bf16x2(acc[6] * inv, acc[7] * inv);
   const long seq = row / p.L, t = row - seq * p.L;
-  *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p.o) + (seq * p.seq_stride + t) * p.ldo + h * 64 + c8) = u;
+  T* dst = reinterpret_cast<T*>(p.o) + (seq * p.seq_stride + t) * p.ldo + h * 64 + c8;
+#pragma unroll
+  for (int k = 0; k < 8; k += 4) {
+    const float v[4] = {acc[k] * inv, acc[k + 1] * inv, acc[k + 2] * inv, acc[k + 3] * inv};
+    AttnOps<T>::store4(dst + k, v);
+  }
 }
 
 // Key slices for a long-sequence bf16 launch whose grid would leave the last round of block
@@ -584,6 +607,10 @@ void attention(const Exec& ex, const AttnArgs& a) {
   SPLAT_CHECK(a.ld % ke == 0 && a.ldo % 4 == 0 && a.ld >= (long)a.heads * 64, BAD_ARGUMENT, "attention: strides");
   SPLAT_CHECK(a.seqs == 1 || a.seq_stride >= a.L, BAD_ARGUMENT, "attention: overlapping sequences");
   const bool bf_fast = a.dt != F32 && long(a.L) * a.ld * 2 < 2147483648L && a.ld % 8 == 0 && a.ldo % 4 == 0;
+  // fp32 (and the generic bf16 kernel): one block of 128 queries cannot keep a CU busy (fp32
+  // matrix cores at 1/16 of the bf16 rate), so a small grid is cut into key slices until it
+  // has about two blocks per CU, each slice at least two key tiles (DA3-Small C1: 66 blocks).
+  const long gblocks = long(cdiv(a.L, ATTN_WAVES * 32)) * a.heads * a.seqs;
   // 4 waves x 32 or 64 queries. Two query sub-tiles per wave (QT = 2) halve the K/V reads per
   // query and win once their grid still gives each CU about two blocks (C5 global 2.46 vs
   // 2.85 ms, C4 encoder 56 vs 62 us); below that the doubled block size leaves CUs idle
@@ -592,7 +619,8 @@ void attention(const Exec& ex, const AttnArgs& a) {
   const bool qt2 = blocks2 >= 450;
   const long blocks = qt2 ? blocks2 : long(cdiv(a.L, 128)) * a.heads * a.seqs;
   const int ntiles = cdiv(a.L, 64);
-  const int S = bf_fast && a.L >= 4096 ? attn_splits(blocks, ntiles) : 1;
+  const int S = bf_fast ? (a.L >= 4096 ? attn_splits(blocks, ntiles) : 1)
+                       : int(std::min<long>(std::min<long>(8, ntiles / 2), std::max<long>(1, cdiv(512, gblocks))));
   AttnArgs b = a;
   if (S > 1) {
     b.tps = cdiv(ntiles, S);
@@ -606,25 +634,40 @@ void attention(const Exec& ex, const AttnArgs& a) {
   const double rows = double(a.seqs) * a.L * a.heads;
   ProfScope ps(ex, "attention", 4.0 * rows * a.L * 64, 4.0 * rows * 64 * (a.dt == F32 ? 4 : 2));
   const float c = 0.125f * 1.4426950408889634f;
-  if (a.dt == F32) {
-    dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
-    hipLaunchKernelGGL(attn_kernel<float>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);
-  } else if (bf_fast) {
+  if (!bf_fast) {
+    const dim3 grid(unsigned(cdiv(a.L, ATTN_WAVES * 32) * b.nsplit), a.heads, a.seqs);
+    const long work = long(a.seqs) * a.L * a.heads * 8;
+    const dim3 cgrid(unsigned((work + 255) / 256));
+    if (a.dt == F32) {
+      if (b.nsplit > 1) {
+        hipLaunchKernelGGL((attn_kernel<float, true>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
+        SPLAT_HIP(hipGetLastError());
+        hipLaunchKernelGGL(attn_combine_kernel<float>, cgrid, dim3(256), 0, ex.stream, b);
+      } else {
+        hipLaunchKernelGGL((attn_kernel<float, false>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
+      }
+    } else {
+      if (b.nsplit > 1) {
+        hipLaunchKernelGGL((attn_kernel<bf16, true>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
+        SPLAT_HIP(hipGetLastError());
+        hipLaunchKernelGGL(attn_combine_kernel<bf16>, cgrid, dim3(256), 0, ex.stream, b);
+      } else {
+        hipLaunchKernelGGL((attn_kernel<bf16, false>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
+      }
+    }
+  } else {
     const dim3 grid(unsigned(blocks * b.nsplit));
     if (b.nsplit > 1) {
       if (qt2) hipLaunchKernelGGL((attn_bf16_kernel<4, 2, true>), grid, dim3(256), 0, ex.stream, b, c);
       else hipLaunchKernelGGL((attn_bf16_kernel<4, 1, true>), grid, dim3(256), 0, ex.stream, b, c);
       SPLAT_HIP(hipGetLastError());
       const long work = long(a.seqs) * a.L * a.heads * 8;
-      hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b);
+      hipLaunchKernelGGL(attn_combine_kernel<bf16>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b);
     } else if (qt2) {
       hipLaunchKernelGGL((attn_bf16_kernel<4, 2, false>), grid, dim3(256), 0, ex.stream, b, c);
     } else {
       hipLaunchKernelGGL((attn_bf16_kernel<4, 1, false>), grid, dim3(256), 0, ex.stream, b, c);
     }
-  } else {
-    dim3 grid(cdiv(a.L, ATTN_WAVES * 32), a.heads, a.seqs);
-    hipLaunchKernelGGL(attn_kernel<bf16>, grid, dim3(ATTN_WAVES * 64), 0, ex.stream, a, c);
   }
   SPLAT_HIP(hipGetLastError());
 }
