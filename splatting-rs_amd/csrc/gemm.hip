@@ -171,7 +171,7 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
 // block must be past its last read of the main-loop LDS.
 // EPI_PART: split-K slice, the raw fp32 sums go to the partial buffer; a reduce kernel adds
 // the slices and applies the full epilogue.
-enum EpiKind { EPI_BIAS = 0, EPI_RES = 1, EPI_FULL = 2, EPI_PART = 3 };
+enum EpiKind { EPI_BIAS = 0, EPI_RES = 1, EPI_FULL = 2, EPI_PART = 3, EPI_HEAD = 4 };
 
 constexpr int slab_ld(int tn) { return tn * 32 + 4; }  // +4 floats: conflict-free 16-byte row reads
 
@@ -302,8 +302,89 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
   }
 }
 
+// EPI_HEAD: the MapAnything output head (mapanything-rs/src/dpt.rs:196-198 conv2.2 and
+// model.rs:148-172 dense_output) on the tile's pixels, which hold all N = 128 channels. Each
+// lane takes 8 channels of a slab row: h = bf16(relu(acc + bias)), 6 partial dot products with
+// the 1x1 weights, summed over the row's lanes by DPP; the waves' partials per row meet in LDS
+// after the slabs (the ring is free by then), and one thread per pixel finishes the outputs.
+template <typename T, int BM, int BN, int WM, int WN, int TM, int TN>
+__device__ __forceinline__ void head_epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long m0, int wm, int wn,
+                                              float* smemf, int wave, int lane, int tid) {
+  constexpr int NW = WM * WN, COLS = TN * 32, LD = slab_ld(TN), RUNS = COLS / 8, RPP = 64 / RUNS;
+  static_assert(BN == 128 && (RUNS == 4 || RUNS == 8), "head epilogue: all 128 channels, 4 or 8 lanes a row");
+  float* slab = smemf + wave * 32 * LD;
+  float* part = smemf + NW * 32 * LD;  // [BM][WN][6]
+  const int cc = (lane % RUNS) * 8, rsub = lane / RUNS;
+  const int c0 = wn * (BN / WN) + cc;
+  float wt[6][8], cb[8];
+#pragma unroll
+  for (int o = 0; o < 6; ++o)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) wt[o][k] = p.hw3[o * 128 + c0 + k];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) cb[k] = p.bias[c0 + k];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    stage_slab<TM, TN>(acc, i, slab, lane);
+#pragma unroll
+    for (int t = 0; t < 32 / RPP; ++t) {
+      const int rr = rsub + t * RPP;
+      float v[8];
+      read8(slab + rr * LD + cc, v);
+      float s[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float h = bf2f(f2bf(fmaxf(v[k] + cb[k], 0.f)));
+#pragma unroll
+        for (int o = 0; o < 6; ++o) s[o] = fmaf(wt[o][k], h, s[o]);
+      }
+#pragma unroll
+      for (int o = 0; o < 6; ++o) {
+        s[o] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s[o]), 0xB1, 0xf, 0xf, true));
+        s[o] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s[o]), 0x4E, 0xf, 0xf, true));
+        if (RUNS == 8) s[o] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s[o]), 0x141, 0xf, 0xf, true));
+      }
+      if (lane % RUNS == 0) {
+        float* dst = part + ((wm * (BM / WM) + i * 32 + rr) * WN + wn) * 6;
+#pragma unroll
+        for (int o = 0; o < 6; ++o) dst[o] = s[o];
+      }
+    }
+    slab_done();
+  }
+  __syncthreads();
+  const float sc = p.hscale ? *p.hscale : 1.f;
+  for (int r = tid; r < BM; r += NW * 64) {
+    const long px = m0 + r;
+    if (px >= p.M) continue;
+    float raw[6];
+#pragma unroll
+    for (int o = 0; o < 6; ++o) {
+      float acc6 = p.hb3[o];
+#pragma unroll
+      for (int w = 0; w < WN; ++w) acc6 += part[(r * WN + w) * 6 + o];
+      raw[o] = acc6;
+    }
+    const long v = px / p.hhw, q = px - v * p.hhw;
+    if (p.ho0) {
+#pragma unroll
+      for (int o = 0; o < 6; ++o) p.ho0[(v * 6 + o) * p.hhw + q] = raw[o];
+    }
+    // mapanything-rs/src/model.rs:155-168
+    const float nrm = fmaxf(sqrtf(raw[0] * raw[0] + raw[1] * raw[1] + raw[2] * raw[2]), 1e-8f);
+    const float depth = expf(raw[3]) * sc;
+    if (p.ho1) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) p.ho1[px * 3 + j] = raw[j] / nrm * depth;
+    }
+    if (p.ho2) p.ho2[px] = 1.f + expf(raw[4]);
+    if (p.ho3) p.ho3[px] = raw[5] > 0.f ? 1 : 0;
+  }
+}
+
 // Which epilogue variant a launch needs (host side; `a.epi_vec` already set).
 inline int epi_kind(const GemmArgs& a) {
+  if (a.hw3) return EPI_HEAD;
   if (!a.epi_vec || a.rm_P || a.store != STORE_ROWS || a.addtab || a.act_post || (a.res2 && !a.res)) return EPI_FULL;
   return (a.res || a.gamma) ? EPI_RES : EPI_BIAS;
 }
@@ -752,9 +833,14 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs 
   tile(nk - 1, std::false_type{}, std::false_type{});
   wait_vmcnt<0>();  // the zero-fill loads past the last tile must land before the ring is reused
   __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
-  float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
-  epilogue<T, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
-                              EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr);
+  if constexpr (EPI == EPI_HEAD) {
+    static_assert(NW * 32 * slab_ld(TN) * 4 + BM * WN * 6 * 4 <= STAGES * STAGE, "head epilogue LDS");
+    head_epilogue<T, BM, BN, WM, WN, TM, TN>(p, acc, m0, wm, wn, reinterpret_cast<float*>(smem), wave, lane, tid);
+  } else {
+    float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
+    epilogue<T, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
+                                EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr);
+  }
 }
 
 // Split-K reduction: out = epilogue(sum over slices of the fp32 partials), 8 columns a thread.
@@ -797,7 +883,11 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   const bool tap = a.amode == A_CONV && a.Cin % BK == 0 && a.ks * a.ks <= 32;
   SPLAT_CHECK(a.amode == A_ROWS || tap || !a.relu_in, BAD_ARGUMENT,
               "gemm: ReLU-on-load needs a convolution whose Cin is a multiple of the k-tile");
-  if (a.amode == A_ROWS) {
+  if (epi == EPI_HEAD) {  // the fused MapAnything head: one tile spans the 128 channels
+    SPLAT_CHECK(tap && !a.relu_in && a.N == BN && a.act == ACT_RELU && S == 1, BAD_ARGUMENT, "gemm: fused head");
+    if constexpr (BN == 128 && sizeof(T) == 2) SPLAT_GO(A_CONV_TAP, false, EPI_HEAD);
+    else SPLAT_CHECK(false, BAD_ARGUMENT, "gemm: fused head needs a bf16 128-column tile");
+  } else if (a.amode == A_ROWS) {
     if (epi == EPI_PART) SPLAT_GO(A_ROWS, false, EPI_PART);
     else if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
     else if (epi == EPI_RES) SPLAT_GO(A_ROWS, false, EPI_RES);
@@ -867,9 +957,10 @@ static BfCfg pick_bf16(const GemmArgs& a) {
   const BfCfg cands[] = {CFG_256x256, CFG_256x128, CFG_320x256, CFG_320x128, CFG_192x128, CFG_128x128};
   const double eff[] = {1.0, 0.80, 1.0, 0.80, 0.75, 0.65};
   double best = 1e30;
-  BfCfg pick = CFG_256x256;
+  BfCfg pick = a.hw3 ? CFG_320x128 : CFG_256x256;
   for (int i = 0; i < 6; ++i) {
     const BfShape sh = bf_shape(cands[i]);
+    if (a.hw3 && sh.bn != 128) continue;  // the fused head needs the 128 channels in one tile
     const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
     const long rounds = (tiles + GEMM_CUS - 1) / GEMM_CUS;
     const double cost = double(rounds) * sh.bm * sh.bn / eff[i];
@@ -883,6 +974,7 @@ static BfCfg pick_bf16(const GemmArgs& a) {
 // one round. The slices write fp32 partials; a second kernel sums them and applies the
 // epilogue (the DPT head's coarse-level convs: M = 1596, K = 6912, 14 tiles of 256x128).
 static int split_factor(const GemmArgs& a, BfCfg c) {
+  if (a.hw3) return 1;  // the fused head needs whole tiles
   const BfShape sh = bf_shape(c);
   const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
   const long slots = long(GEMM_CUS) * sh.per_cu;
@@ -964,6 +1056,7 @@ static bool mfma_path_ok(const GemmArgs& a) {
 template <typename T>
 static void launch_typed(const Exec& ex, const GemmArgs& a) {
   if (mfma_path_ok(a)) return sizeof(T) == 2 ? launch_bf16_auto(ex, a) : launch_f32_auto(ex, a);
+  SPLAT_CHECK(a.hw3 == nullptr, BAD_ARGUMENT, "gemm: the fused head needs the MFMA path");
   const long tiles128 = (long)cdiv(a.M, 128) * cdiv(a.N, 128);
   if (a.N <= 32) launch_cfg<T, 256, 32, 4, 1>(ex, a);
   else if (a.N <= 64) launch_cfg<T, 256, 64, 4, 1>(ex, a);

@@ -46,6 +46,12 @@ struct GemmArgs {
   int epi_vec = 0;  // set by gemm(): the epilogue may use 16-byte vector accesses
   // Set by gemm() for a split-K launch: fp32 partial sums [splits][M][ldp], kper k-tiles each.
   float* part = nullptr; long ldp = 0; int kper = 0;
+  // MapAnything output head fused into the epilogue (bf16 convolution with N = 128, act ReLU):
+  // h = relu(acc + bias) rounded to bf16 as a stored map would be, raw = hw3 [6, 128] h + hb3,
+  // then what pointwise_head(PW_MA) writes from raw: ho0 raw NCHW [V, 6, hhw], ho1 points
+  // [pix, 3] (scaled by *hscale), ho2 confidence, ho3 unambiguous mask (each may be null).
+  const float* hw3 = nullptr; const float* hb3 = nullptr; const float* hscale = nullptr; int hhw = 0;
+  float* ho0 = nullptr; float* ho1 = nullptr; float* ho2 = nullptr; uint8_t* ho3 = nullptr;
 };
 void gemm(const Exec& ex, const GemmArgs& a);
 

@@ -318,12 +318,28 @@ void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_o
     gemm(ex, conv_args(head1_, dt_, path, V, FH, FW, 1, h1));
     void* up = ar.alloc(size_t(V) * H * W * (F / 2) * es);
     resize_bilinear(ex, dt_, h1, V, FH, FW, F / 2, up, H, W, H, W, nullptr, 0);
-    void* h2 = ar.alloc(size_t(V) * H * W * (F / 2) * es);
-    GemmArgs g = conv_args(head2_, dt_, up, V, H, W, 1, h2);
+    GemmArgs g = conv_args(head2_, dt_, up, V, H, W, 1, nullptr);
     g.act = ACT_RELU;
-    gemm(ex, g);
-    pointwise_head(ex, dt_, PW_MA, h2, long(V) * H * W, H * W, F / 2, 6, head3_w_, head3_b_, out.raw, out.points,
-                   out.conf, out.mask, scale);
+    if (dt_ == BF16 && F / 2 == 128 && head2_.cin % 64 == 0) {
+      // 1x1 head and dense_output in the convolution's epilogue: the 128-channel map at full
+      // resolution (312 MB at C4) is never written
+      g.out = up;  // not written
+      g.hw3 = head3_w_;
+      g.hb3 = head3_b_;
+      g.hscale = scale;
+      g.hhw = H * W;
+      g.ho0 = out.raw;
+      g.ho1 = out.points;
+      g.ho2 = out.conf;
+      g.ho3 = out.mask;
+      gemm(ex, g);
+    } else {
+      void* h2 = ar.alloc(size_t(V) * H * W * (F / 2) * es);
+      g.out = h2;
+      gemm(ex, g);
+      pointwise_head(ex, dt_, PW_MA, h2, long(V) * H * W, H * W, F / 2, 6, head3_w_, head3_b_, out.raw, out.points,
+                     out.conf, out.mask, scale);
+    }
     ar.release(mdpt);
   }
 

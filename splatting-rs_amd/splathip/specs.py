@@ -104,6 +104,10 @@ MA_SPECS = {
     "tiny_proj": MaSpec("tiny_proj", 192, 3, 3, FFN_MLP, 768, 128, 2, 4, FFN_SWIGLU,
                         swiglu_hidden_dim(128), (1, 2, 3),
                         dpt_dims=(32, 64, 96, 128), dpt_features=64, pose_dim=96, scale_dim=48),
+    # The tiny transformer with the reference's 256-feature DPT head (its 128-channel output
+    # convolution is the one whose epilogue runs the output head in bf16).
+    "tiny_f256": MaSpec("tiny_f256", 128, 2, 3, FFN_MLP, 512, 128, 2, 4, FFN_MLP, 512, (1, 2, 3),
+                        dpt_dims=(32, 64, 96, 128), dpt_features=256, pose_dim=96, scale_dim=48),
 }
 
 

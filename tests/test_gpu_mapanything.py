@@ -67,6 +67,32 @@ def test_ma_tiny_fp32(ctx, ma_weights, name, ls):
         assert cosine(a, b.numpy()) > 0.99999, i
 
 
+def test_ma_head_fused_bf16(ctx, weights_dir):
+    """The 256-feature DPT head in bf16: its 128-channel output convolution computes the 1x1
+    head and dense_output in its epilogue (no stored map); outputs against the oracle."""
+    spec = specs.MA_SPECS["tiny_f256"]
+    w = synth.generate(synth.ma_shapes(spec), seed=23, layer_scale=1.0)
+    path = os.path.join(str(weights_dir), "ma_tiny_f256.safetensors")
+    synth.save(path, w)
+    images = synth.procedural_images(3, 56, 70, seed=9)
+    report("ma.head_fused.bf16")
+    ctx.load_mapanything(path, spec, "bf16")
+    out = ctx.ma_forward(images)
+    ref = O.forward(w, spec, images)
+    depth = np.exp(out["raw"][:, 3]) * out["scale"][0]
+    rdepth = np.exp(ref["raw"][:, 3].numpy()) * ref["scale"]
+    med = float(np.median(np.abs(depth / rdepth - 1)))
+    craw = cosine(out["raw"], ref["raw"].numpy())
+    cpts = cosine(out["points"], ref["points"].permute(0, 2, 3, 1).numpy())
+    cconf = cosine(out["conf"], ref["conf"].numpy())
+    agree = float(np.mean(out["mask"].astype(bool) == ref["mask"].numpy()))
+    report("ma.head_fused.bf16.errs", depth_median_rel=f"{med:.2e}", raw_cos=f"{craw:.6f}", points_cos=f"{cpts:.6f}",
+           conf_cos=f"{cconf:.6f}", mask_agree=f"{agree:.4f}")
+    assert med <= 1e-2
+    assert craw >= 0.999 and cpts >= 0.999 and cconf >= 0.999
+    assert agree >= 0.99
+
+
 @pytest.mark.parametrize("name", ["tiny", "tiny_proj"])
 def test_ma_tiny_bf16(ctx, ma_weights, name):
     path, w, spec = ma_weights[(name, 1.0)]
