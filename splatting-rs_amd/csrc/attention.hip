@@ -305,7 +305,7 @@ template <int N> __device__ inline void wait_vm() { asm volatile("s_waitcnt vmcn
 // SPLIT: the block covers key tiles [split * tps, (split + 1) * tps) of its sequence and writes
 // its unnormalised O and (max, sum) to p.part; attn_combine_kernel merges the slices.
 template <int WAVES, int QT, bool SPLIT>
-__global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs p, float c) {
+__global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(const AttnArgs p, float c) {
   constexpr int KBYTES = 64 * 128;            // K or V tile: 64 keys x 128 bytes, swizzled, unpadded
   constexpr int KL = 8 / WAVES;               // load instructions per wave per K (or V) tile
   static_assert(WAVES == 2 || WAVES == 4, "the load swizzles assume an even number of waves");
@@ -329,6 +329,10 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + h * 64;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + h * 64;
   const int q0 = (qb * WAVES + wave) * (QT * 32);
+  // A wave whose queries all lie past the sequence (the last query block of a 1037-token view
+  // has 13) still loads its share of every K/V tile and meets every barrier, but computes
+  // nothing: the other waves on its SIMD get the matrix core and the VALU.
+  const bool active = __builtin_amdgcn_readfirstlane(q0) < L;
 
   uint4 qf[QT][4];
 #pragma unroll
@@ -503,14 +507,14 @@ __global__ void __launch_bounds__(WAVES * 64, 2) attn_bf16_kernel(const AttnArgs
     const int b = (t - t0) & 1;
     issue_k(t + 1, b ^ 1);
     issue_v(t + 1, b ^ 1);
-    tile(t, b, b, std::false_type{});
+    if (active) tile(t, b, b, std::false_type{});
     wait_vm<0>();  // this wave's share of tile t+1
     __syncthreads();
   }
   // the slice's last tile, with the key mask (a no-op unless it holds the sequence's ragged
   // end): one peeled copy, as a second one (unmasked) cost 50 more VGPRs and half the occupancy
   const int bl = (t1 - 1 - t0) & 1;
-  tile(t1 - 1, bl, bl, std::true_type{});
+  if (active) tile(t1 - 1, bl, bl, std::true_type{});
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
