@@ -146,7 +146,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the network would "
-              "shard by views with one K/V exchange per global block; see DESIGN.md). Run with --gpus 1.",
+              "shard by views with one K/V exchange per global block). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
