@@ -292,11 +292,16 @@ __device__ inline int32x4_t make_rsrc_a(const void* p, uint32_t bytes) {
   return r;
 }
 
-__device__ inline void load_lds_a(const int32x4_t& rsrc, uint32_t voffset, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(__builtin_amdgcn_readfirstlane(int(lds))),
-               "v"(voffset), "s"(rsrc)
+// 16 bytes per lane from rsrc at voffset + soffset into LDS at lds + 16 * lane. A voffset of
+// 0x80000000 reads zeros whatever soffset holds: every valid voffset + soffset lies inside the
+// buffer (below 2^31), so the range check, with or without soffset, rejects only that one.
+__device__ inline void load_lds_a(const int32x4_t& rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(__builtin_amdgcn_readfirstlane(int(lds))),
+               "v"(voffset), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(int(soffset)))
                : "memory");
 }
+
+__device__ inline float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
 template <int N> __device__ inline void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
@@ -314,7 +319,8 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   // is bound by its VALU work, not by load latency.
   __shared__ __attribute__((aligned(1024))) char smem[4 * KBYTES];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index is uniform, so every LDS destination of the DMA loads is scalar arithmetic
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int L = p.L;
   // 1D grid over (query block, head, sequence), query blocks fastest; the query blocks of one
@@ -344,32 +350,45 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
                             : make_uint4(0, 0, 0, 0);
   }
 
-  // K rows: sequence row s -> byte offset within the buffer that starts at the sequence's row 0
+  // K and V rows: sequence row s -> byte offset within the buffer that starts at the
+  // sequence's row 0. Lane offsets within a tile are fixed; the tile's t * 64 rows go in the
+  // scalar offset, and only a tile that reaches past L checks its rows.
   const bf16* Kseq = reinterpret_cast<const bf16*>(p.k) + base * p.ld + h * 64;
   const int32x4_t rk = make_rsrc_a(Kseq, uint32_t(long(L) * p.ld * 2));
-  const int lrow = lane >> 3;
-  const int kc = (lane & 7) ^ ((4 * (wave & 1) + (lrow >> 1)) & 7);
-  auto issue_k = [&](int t, int buf) {
-    const uint32_t sb = uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_a)(smem + buf * KBYTES)));
-#pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int row = (i * WAVES + wave) * 8 + lrow;
-      const int key = t * 64 + row;
-      load_lds_a(rk, key < L ? uint32_t(key * p.ld * 2 + kc * 16) : 0x80000000u, sb + (i * WAVES + wave) * 1024);
-    }
-  };
   // V rows: chunk c of row r in slot c ^ (2 * (r & 3)), so that the four consecutive rows one
   // 16-lane group of a transposed read touches sit on four different 32-byte bank groups.
   const bf16* Vseq = V + base * p.ld;
   const int32x4_t rv = make_rsrc_a(Vseq, uint32_t(long(L) * p.ld * 2));
+  const int lrow = lane >> 3;
+  const int kc = (lane & 7) ^ ((4 * (wave & 1) + (lrow >> 1)) & 7);
   const int vc = (lane & 7) ^ ((lrow & 3) << 1);
-  auto issue_v = [&](int t, int buf) {
-    const uint32_t sb = uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_a)(smem + (2 + buf) * KBYTES)));
+  const uint32_t tile_bytes = uint32_t(64 * p.ld * 2);
+  int lrw[KL];
+  uint32_t koff[KL], voff[KL];
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int row = (i * WAVES + wave) * 8 + lrow;
-      const int key = t * 64 + row;
-      load_lds_a(rv, key < L ? uint32_t(key * p.ld * 2 + vc * 16) : 0x80000000u, sb + (i * WAVES + wave) * 1024);
+  for (int i = 0; i < KL; ++i) {
+    lrw[i] = (i * WAVES + wave) * 8 + lrow;
+    koff[i] = uint32_t(lrw[i] * p.ld * 2 + kc * 16);
+    voff[i] = uint32_t(lrw[i] * p.ld * 2 + vc * 16);
+  }
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_a)smem));
+  // K and V of tile t into ring slot B (compile time: the LDS destinations are constants)
+  auto issue = [&](int t, auto bufc) {
+    constexpr int B = decltype(bufc)::value;
+    const uint32_t so = uint32_t(t) * tile_bytes;
+    if (t * 64 + 64 <= L) {
+#pragma unroll
+      for (int i = 0; i < KL; ++i) {
+        load_lds_a(rk, koff[i], so, lds0 + B * KBYTES + (i * WAVES + wave) * 1024);
+        load_lds_a(rv, voff[i], so, lds0 + (2 + B) * KBYTES + (i * WAVES + wave) * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < KL; ++i) {
+        const bool in = t * 64 + lrw[i] < L;
+        load_lds_a(rk, in ? koff[i] : 0x80000000u, so, lds0 + B * KBYTES + (i * WAVES + wave) * 1024);
+        load_lds_a(rv, in ? voff[i] : 0x80000000u, so, lds0 + (2 + B) * KBYTES + (i * WAVES + wave) * 1024);
+      }
     }
   };
   // A operand of O^T[d][q] += V^T[d][keys] P^T[keys][q] for keys kt2*32 + 16*hh + (0..31): lane
@@ -407,10 +426,11 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   }
   const int sw = (l32 >> 1) & 7;
 
-  auto tile = [&](int t, int kbuf, int vbuf, auto masked_t) {
+  auto tile = [&](int t, auto bufc, auto masked_t) {
     constexpr bool masked = decltype(masked_t)::value;
-    const char* kb = smem + kbuf * KBYTES;
-    const char* vt = smem + (2 + vbuf) * KBYTES;
+    constexpr int B = decltype(bufc)::value;
+    const char* kb = smem + B * KBYTES;
+    const char* vt = smem + (2 + B) * KBYTES;
     f32x16 s[QT][2];
     const f32x16 zero = {};
 #pragma unroll
@@ -438,12 +458,18 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
     float mnew[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      // 32 scores -> 1 with three-input maxima (v_max3_f32): 16 instructions
-      float m8[8];
+      // 32 scores -> 1 with three-input maxima (v_max3_f32): 10 + 4 + 2 instructions
+      float a[12];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        m8[i] = fmaxf(fmaxf(s[qt][0][2 * i], s[qt][0][2 * i + 1]), fmaxf(s[qt][1][2 * i], s[qt][1][2 * i + 1]));
-      float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
+      for (int i = 0; i < 5; ++i) {
+        a[i] = max3f(s[qt][0][3 * i], s[qt][0][3 * i + 1], s[qt][0][3 * i + 2]);
+        a[5 + i] = max3f(s[qt][1][3 * i], s[qt][1][3 * i + 1], s[qt][1][3 * i + 2]);
+      }
+      a[10] = s[qt][0][15];
+      a[11] = s[qt][1][15];
+      const float b0 = max3f(a[0], a[1], a[2]), b1 = max3f(a[3], a[4], a[5]), b2 = max3f(a[6], a[7], a[8]),
+                  b3 = max3f(a[9], a[10], a[11]);
+      float mx = fmaxf(max3f(b0, b1, b2), b3);
       // the other half of the query's keys sits in lane l ^ 32: one v_permlane32_swap gives
       // every lane both halves (a ds_bpermute costs an LDS round trip)
       const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
@@ -496,25 +522,35 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
 
   const int ntiles = (L + 63) / 64;
   const int t0 = SPLIT ? split * p.tps : 0, t1 = SPLIT ? min(ntiles, t0 + p.tps) : ntiles;
-  issue_k(t0, 0);
-  issue_v(t0, 0);
+  const std::integral_constant<int, 0> R0;
+  const std::integral_constant<int, 1> R1;
+  issue(t0, R0);
   wait_vm<0>();
   __syncthreads();
   // Every tile but the last runs without the key mask (a runtime flag inside one loop body was
-  // turned into selects that ran on every tile: ~100 VALU instructions per 64-key tile).
-  for (int t = t0; t + 1 < t1; ++t) {
-    // buffers (t+1)&1 held tile t-1, which every wave finished before the last barrier
-    const int b = (t - t0) & 1;
-    issue_k(t + 1, b ^ 1);
-    issue_v(t + 1, b ^ 1);
-    if (active) tile(t, b, b, std::false_type{});
+  // turned into selects that ran on every tile: ~100 VALU instructions per 64-key tile). Tile t
+  // sits in ring slot (t - t0) & 1; the loop is unrolled by two so that the slot, and with it
+  // every LDS address, is a compile-time constant.
+  auto step = [&](int t, auto bufc) {
+    constexpr int B = decltype(bufc)::value;
+    // slot B ^ 1 held tile t-1, which every wave finished before the last barrier
+    issue(t + 1, std::integral_constant<int, B ^ 1>{});
+    if (active) tile(t, bufc, std::false_type{});
     wait_vm<0>();  // this wave's share of tile t+1
     __syncthreads();
+  };
+  int t = t0;
+  for (; t + 2 < t1; t += 2) {
+    step(t, R0);
+    step(t + 1, R1);
   }
+  if (t + 1 < t1) step(t++, R0);
   // the slice's last tile, with the key mask (a no-op unless it holds the sequence's ragged
   // end): one peeled copy, as a second one (unmasked) cost 50 more VGPRs and half the occupancy
-  const int bl = (t1 - 1 - t0) & 1;
-  if (active) tile(t1 - 1, bl, bl, std::true_type{});
+  if (active) {
+    if ((t - t0) & 1) tile(t, R1, std::true_type{});
+    else tile(t, R0, std::true_type{});
+  }
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
