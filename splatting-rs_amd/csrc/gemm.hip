@@ -574,8 +574,10 @@ constexpr int A_CONV_TAP = 2;
 // T = bf16 (one v_mfma_f32_32x32x16_bf16 per k-step) or float (four v_mfma_f32_32x32x2f32):
 // a k-step is 32 bytes of K per row either way, so the tiles, loads and swizzles are the same
 // byte for byte; BK counts elements (128-byte rows: 64 bf16 or 32 fp32).
-template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int AMODE, bool RELU, int EPI>
-__global__ void __launch_bounds__(WM * WN * 64) gemm_mfma_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
+// MINB: blocks per CU the register allocation must allow (2 for a tile whose LDS ring lets two
+// blocks share a CU).
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int AMODE, bool RELU, int EPI, int MINB>
+__global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32, NW = WM * WN;
   constexpr int ES = sizeof(T), KE = 16 / ES;  // bytes per element, elements per 16-byte chunk
   constexpr int MPI = ES == 4 ? 4 : 1;         // MFMA instructions per Mfma<T>::mma
@@ -865,8 +867,9 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p, in
 
 constexpr int GEMM_CUS = 256;  // MI355X compute units: one "round" of resident blocks per CU slot
 
-template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 128 / sizeof(T)>
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 128 / sizeof(T), int MINB = 1>
 static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
+  static_assert(MINB == 1 || MINB * STAGES * (BM + BN) * BK * sizeof(T) <= 160 * 1024, "LDS of MINB blocks per CU");
   const int tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
   const int epi = S > 1 ? EPI_PART : epi_kind(a);
   GemmArgs b = a;
@@ -877,7 +880,8 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   }
   dim3 grid(tm * tn * S);
 #define SPLAT_GO(AM, RL, EP) \
-  hipLaunchKernelGGL((gemm_mfma_kernel<T, BM, BN, WM, WN, STAGES, BK, AM, RL, EP>), grid, dim3(WM * WN * 64), 0, ex.stream, b, tm, tn)
+  hipLaunchKernelGGL((gemm_mfma_kernel<T, BM, BN, WM, WN, STAGES, BK, AM, RL, EP, MINB>), grid, dim3(WM * WN * 64), 0, ex.stream, \
+                     b, tm, tn)
   // Convolutions take the per-tap path (A_CONV_TAP) when Cin is a multiple of the k-tile, else
   // the per-lane im2col arithmetic (A_CONV, without ReLU-on-load: no such caller).
   const bool tap = a.amode == A_CONV && a.Cin % BK == 0 && a.ks * a.ks <= 32;
@@ -921,7 +925,7 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
 
 // Tile configurations of the bf16 path: block tile, and how many blocks share a CU.
 enum BfCfg { CFG_128x32, CFG_128x64, CFG_256x256, CFG_256x128, CFG_320x256, CFG_320x128, CFG_192x128, CFG_128x128,
-             CFG_F128x128, CFG_F64x64 };
+             CFG_F128x128, CFG_F64x64, CFG_192x128D };
 struct BfShape { int bm, bn, per_cu; };
 static BfShape bf_shape(BfCfg c) {
   switch (c) {
@@ -934,6 +938,7 @@ static BfShape bf_shape(BfCfg c) {
     case CFG_192x128: return {192, 128, 1};
     case CFG_F128x128: return {128, 128, 2};
     case CFG_F64x64: return {64, 64, 4};
+    case CFG_192x128D: return {192, 128, 2};
     default: return {128, 128, 1};
   }
 }
@@ -954,6 +959,12 @@ static BfCfg pick_bf16(const GemmArgs& a) {
   // (C2 convs 475 -> 266 us against 256-row tiles with 3-4 stages).
   if (a.N <= 32) return CFG_128x32;
   if (a.N <= 64) return CFG_128x64;
+  // 128-channel convolutions over many tiles (the DPT heads' output convs at full and half
+  // resolution): 192x128 tiles with two stages, 80 KB of LDS, so that two blocks share a CU and
+  // one block's prologue and epilogue overlap the other's main loop. Measured from 1.5 rounds of
+  // such blocks up (3x3, 128 -> 128: M = 173k 75 -> 64 us, 1.2M 475-497 -> 443 us; 256 -> 128 at
+  // M = 398k 321 -> 284 us); below ~100k pixels the smaller tiles lose (25k: 18.4 -> 19.4 us).
+  if (a.amode == A_CONV && a.N == 128 && cdiv(a.M, 192) >= 3 * GEMM_CUS) return CFG_192x128D;
   const BfCfg cands[] = {CFG_256x256, CFG_256x128, CFG_320x256, CFG_320x128, CFG_192x128, CFG_128x128};
   const double eff[] = {1.0, 0.80, 1.0, 0.80, 0.75, 0.65};
   double best = 1e30;
@@ -1032,6 +1043,7 @@ static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
     case CFG_320x256: return launch_mfma<bf16, 320, 256, 2, 4, 2>(ex, a, S);
     case CFG_320x128: return launch_mfma<bf16, 320, 128, 2, 4, 2>(ex, a, S);
     case CFG_192x128: return launch_mfma<bf16, 192, 128, 2, 4, 3>(ex, a, S);
+    case CFG_192x128D: return launch_mfma<bf16, 192, 128, 2, 4, 2, 64, 2>(ex, a, S);
     default: return launch_mfma<bf16, 128, 128, 2, 2, 4>(ex, a, S);
   }
 }

@@ -148,6 +148,10 @@ CONV_CASES = [
     # split-K: the DPT head's coarsest level (M = 1596, K = 6912) and a narrow conv
     (6, 19, 14, 768, 256, 3, 1, 0, 0, True),
     (2, 9, 7, 512, 64, 3, 1, 1, 1, False),
+    # 128 output channels over >= 768 tiles of 192 rows: the two-blocks-per-CU tile (bf16),
+    # bias + ReLU epilogue, then ReLU-on-load with a residual (the full epilogue)
+    (3, 224, 224, 64, 128, 3, 1, 0, 1, False),
+    (3, 224, 224, 64, 128, 3, 1, 1, 0, True),
 ]
 
 

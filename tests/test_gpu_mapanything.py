@@ -67,15 +67,17 @@ def test_ma_tiny_fp32(ctx, ma_weights, name, ls):
         assert cosine(a, b.numpy()) > 0.99999, i
 
 
-def test_ma_head_fused_bf16(ctx, weights_dir):
+@pytest.mark.parametrize("hw", [(56, 70), (224, 224)])
+def test_ma_head_fused_bf16(ctx, weights_dir, hw):
     """The 256-feature DPT head in bf16: its 128-channel output convolution computes the 1x1
-    head and dense_output in its epilogue (no stored map); outputs against the oracle."""
+    head and dense_output in its epilogue (no stored map); outputs against the oracle. At
+    3x224x224 (150k pixels) the convolution runs on the two-blocks-per-CU 192x128 tiles."""
     spec = specs.MA_SPECS["tiny_f256"]
     w = synth.generate(synth.ma_shapes(spec), seed=23, layer_scale=1.0)
     path = os.path.join(str(weights_dir), "ma_tiny_f256.safetensors")
     synth.save(path, w)
-    images = synth.procedural_images(3, 56, 70, seed=9)
-    report("ma.head_fused.bf16")
+    images = synth.procedural_images(3, hw[0], hw[1], seed=9)
+    report("ma.head_fused.bf16", hw=hw)
     ctx.load_mapanything(path, spec, "bf16")
     out = ctx.ma_forward(images)
     ref = O.forward(w, spec, images)
