@@ -730,7 +730,7 @@ void small_linear(const Exec& ex, int wdt, const float* x, long ldx, int M, int 
 // unit token, each min-max scaled, balance = sum |x - 0.5|, first argmin.
 constexpr int REF_MAX_VIEWS = 64;
 
-__global__ void ref_view_kernel(const float* xs, int V, int n, int dim, int strategy, int* ref) {
+__global__ void __launch_bounds__(1024) ref_view_kernel(const float* xs, int V, int n, int dim, int strategy, int* ref) {
   __shared__ double gram[REF_MAX_VIEWS * REF_MAX_VIEWS];
   __shared__ double rsum[REF_MAX_VIEWS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -742,18 +742,21 @@ __global__ void ref_view_kernel(const float* xs, int V, int n, int dim, int stra
     if (threadIdx.x == 0) *ref = V / 2;
     return;
   }
-  for (int pq = wave; pq < V * V + V; pq += nw) {
+  // the V(V+1)/2 pairs j >= i of the Gram matrix, then the V row sums, one wave each
+  const int npair = V * (V + 1) / 2;
+  for (int pq = wave; pq < npair + V; pq += nw) {
     double s = 0.0;
-    if (pq < V * V) {
-      const int i = pq / V, j = pq % V;
-      if (j < i) continue;
+    if (pq < npair) {
+      int i = 0, r = pq;
+      while (r >= V - i) { r -= V - i; ++i; }
+      const int j = i + r;
       const float* a = xs + (long)i * n * dim;
       const float* b = xs + (long)j * n * dim;
       for (int c = lane; c < dim; c += 64) s += double(a[c]) * double(b[c]);
       s = wave_sum_d(s);
       if (lane == 0) { gram[i * V + j] = s; gram[j * V + i] = s; }
     } else {
-      const int i = pq - V * V;
+      const int i = pq - npair;
       const float* a = xs + (long)i * n * dim;
       for (int c = lane; c < dim; c += 64) s += double(a[c]);
       s = wave_sum_d(s);
@@ -790,7 +793,7 @@ __global__ void ref_view_kernel(const float* xs, int V, int n, int dim, int stra
 void select_reference_view(const Exec& ex, const float* xs, int V, int n, int dim, int strategy, int* ref) {
   SPLAT_CHECK(V <= REF_MAX_VIEWS, BAD_SHAPE, "reference-view selection supports at most 64 views");
   if (ex.dry) return;
-  hipLaunchKernelGGL(ref_view_kernel, dim3(1), dim3(256), 0, ex.stream, xs, V, n, dim, strategy, ref);
+  hipLaunchKernelGGL(ref_view_kernel, dim3(1), dim3(1024), 0, ex.stream, xs, V, n, dim, strategy, ref);
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -809,9 +812,14 @@ void set_camera_tokens(const Exec& ex, float* xs, int V, int n, int dim, const f
 
 // ---------------------------------------------------------------------------------------
 // depthanything3-rs/src/backbone.rs:177-189 + the dense head's input norm (dpt.rs:277).
+// One wave per token: the row of the current output (xs) and of the layer output kept
+// (within) are read once, as float2 runs of 128 channels per wave (dim is a multiple of 128 in
+// every DA3 variant, at most HOOK_RUNS * 128), and both norms are taken from registers.
+constexpr int HOOK_RUNS = 12;
 template <typename T>
-__global__ void da3_hook_kernel(const float* within, const float* xs, int V, int n, int dim, const float* bnw,
-                                const float* bnb, const float* hnw, const float* hnb, void* out, float* cam_out) {
+__global__ void __launch_bounds__(256) da3_hook_kernel(const float* within, const float* xs, int V, int n, int dim,
+                                                       const float* bnw, const float* bnb, const float* hnw,
+                                                       const float* hnb, void* out, float* cam_out) {
   const long wave = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
   if (wave >= (long)V * n) return;
@@ -826,33 +834,60 @@ __global__ void da3_hook_kernel(const float* within, const float* xs, int V, int
       }
     return;
   }
-  // backbone norm of the current output (eps 1e-5)
+  const int runs = dim >> 7;
+  float2 av[HOOK_RUNS], wv[HOOK_RUNS];
   float s = 0.f;
-  for (int c = lane; c < dim; c += 64) s += a[c];
+#pragma unroll
+  for (int k = 0; k < HOOK_RUNS; ++k)
+    if (k < runs) {
+      av[k] = *reinterpret_cast<const float2*>(a + k * 128 + 2 * lane);
+      wv[k] = *reinterpret_cast<const float2*>(w + k * 128 + 2 * lane);
+      s += av[k].x + av[k].y;
+    }
+  // backbone norm of the current output (eps 1e-5)
   const float am = wave_sum(s) / dim;
   float q = 0.f;
-  for (int c = lane; c < dim; c += 64) { const float d = a[c] - am; q += d * d; }
+#pragma unroll
+  for (int k = 0; k < HOOK_RUNS; ++k)
+    if (k < runs) {
+      const float d0 = av[k].x - am, d1 = av[k].y - am;
+      q += d0 * d0 + d1 * d1;
+    }
   const float ar = rsqrtf(wave_sum(q) / dim + 1e-5f);
-  // head norm over cat(within, normed) (eps 1e-5)
+  // head norm over cat(within, normed) (eps 1e-5); av becomes the normed output
   s = 0.f;
-  for (int c = lane; c < dim; c += 64) s += w[c] + ((a[c] - am) * ar * bnw[c] + bnb[c]);
+#pragma unroll
+  for (int k = 0; k < HOOK_RUNS; ++k)
+    if (k < runs) {
+      const int c = k * 128 + 2 * lane;
+      av[k].x = (av[k].x - am) * ar * bnw[c] + bnb[c];
+      av[k].y = (av[k].y - am) * ar * bnw[c + 1] + bnb[c + 1];
+      s += wv[k].x + wv[k].y + av[k].x + av[k].y;
+    }
   const float hm = wave_sum(s) / (2 * dim);
   q = 0.f;
-  for (int c = lane; c < dim; c += 64) {
-    const float d0 = w[c] - hm, d1 = (a[c] - am) * ar * bnw[c] + bnb[c] - hm;
-    q += d0 * d0 + d1 * d1;
-  }
+#pragma unroll
+  for (int k = 0; k < HOOK_RUNS; ++k)
+    if (k < runs) {
+      const float d0 = wv[k].x - hm, d1 = wv[k].y - hm, d2 = av[k].x - hm, d3 = av[k].y - hm;
+      q += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
+    }
   const float hr = rsqrtf(wave_sum(q) / (2 * dim) + 1e-5f);
   const long ob = ((long)v * (n - 1) + t - 1) * 2 * dim;
-  for (int c = lane; c < dim; c += 64) {
-    const float an = (a[c] - am) * ar * bnw[c] + bnb[c];
-    st<T>(out, ob + c, (w[c] - hm) * hr * hnw[c] + hnb[c]);
-    st<T>(out, ob + dim + c, (an - hm) * hr * hnw[dim + c] + hnb[dim + c]);
-  }
+#pragma unroll
+  for (int k = 0; k < HOOK_RUNS; ++k)
+    if (k < runs) {
+      const int c = k * 128 + 2 * lane;
+      st<T>(out, ob + c, (wv[k].x - hm) * hr * hnw[c] + hnb[c]);
+      st<T>(out, ob + c + 1, (wv[k].y - hm) * hr * hnw[c + 1] + hnb[c + 1]);
+      st<T>(out, ob + dim + c, (av[k].x - hm) * hr * hnw[dim + c] + hnb[dim + c]);
+      st<T>(out, ob + dim + c + 1, (av[k].y - hm) * hr * hnw[dim + c + 1] + hnb[dim + c + 1]);
+    }
 }
 
 void da3_hook(const Exec& ex, int dt, const float* within, const float* xs, int V, int n, int dim, const float* bnw,
               const float* bnb, const float* hnw, const float* hnb, void* out, float* cam_out) {
+  SPLAT_CHECK(dim % 128 == 0 && dim <= HOOK_RUNS * 128, BAD_SHAPE, "da3_hook: dim must be a multiple of 128, at most 1536");
   if (ex.dry) return;
   ProfScope ps(ex, "da3_hook", 0, double(V) * n * dim * 8 + double(V) * (n - 1) * 2 * dim * dtype_size(dt));
   dim3 grid(cdiv((long)V * n, 4));
