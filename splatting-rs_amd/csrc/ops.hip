@@ -313,7 +313,10 @@ __global__ void resize_kernel(const void* in, int V, int Hi, int Wi, int C, void
 // and written as 8-channel vectors (one 16-byte access per pixel for bf16). One block row per
 // output row (grid.y = V*Ho), so the row's source rows and weight follow from blockIdx.y and the
 // per-thread index math is 32-bit (C4's five resizes 295 -> 230 us against a flat 64-bit index
-// decomposition with 8-byte accesses).
+// decomposition with 8-byte accesses). A thread covers RESIZE_ROWS output rows of one column, so
+// the column's source coordinate is computed once; coordinates are f64 products with the scale
+// (in - 1) / (out - 1) computed on the host (the f64 division per thread and row was most of
+// the kernel's instructions).
 template <typename T> struct Vec8;
 template <> struct Vec8<bf16> {
   __device__ static inline void load(const void* p, long i, float* v) {
@@ -347,37 +350,45 @@ template <> struct Vec8<float> {
   }
 };
 
+constexpr int RESIZE_ROWS = 4;
 template <typename T>
-__global__ void __launch_bounds__(256) resize8_kernel(const void* in, int Hi, int Wi, int C, void* out, int Hf, int Wf,
-                                                      int Ho, int Wo, const float* addtab, int relu) {
+__global__ void __launch_bounds__(256) resize8_kernel(const void* in, int Hi, int Wi, int C, void* out, int Ho, int Wo,
+                                                      int rows, double sy, double sx, const float* addtab, int relu) {
   const int C8 = C >> 3;
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= Wo * C8) return;
-  const int row = blockIdx.y, v = row / Ho, oy = row - v * Ho;
   const int ox = t / C8, c = (t - ox * C8) * 8;
-  const double fy = Hf > 1 ? double(Hi - 1) * oy / double(Hf - 1) : 0.0;
-  const double fx = Wf > 1 ? double(Wi - 1) * ox / double(Wf - 1) : 0.0;
-  const int y0 = min(int(fy), Hi - 1), x0 = min(int(fx), Wi - 1);
-  const int y1 = y0 + (y0 < Hi - 1 ? 1 : 0), x1 = x0 + (x0 < Wi - 1 ? 1 : 0);
-  const float ly = float(fy - y0), lx = float(fx - x0);
-  const long b = long(v) * Hi * Wi;
-  float a[8], bq[8], cq[8], d[8], y[8];
-  Vec8<T>::load(in, (b + long(y0) * Wi + x0) * C + c, a);
-  Vec8<T>::load(in, (b + long(y0) * Wi + x1) * C + c, bq);
-  Vec8<T>::load(in, (b + long(y1) * Wi + x0) * C + c, cq);
-  Vec8<T>::load(in, (b + long(y1) * Wi + x1) * C + c, d);
+  const double fx = sx * ox;
+  const int x0 = min(int(fx), Wi - 1);
+  const int x1 = x0 + (x0 < Wi - 1 ? 1 : 0);
+  const float lx = float(fx - x0);
+  for (int r = 0; r < RESIZE_ROWS; ++r) {
+    const int row = blockIdx.y * RESIZE_ROWS + r;  // over V * Ho output rows
+    if (row >= rows) break;
+    const int v = row / Ho, oy = row - v * Ho;
+    const double fy = sy * oy;
+    const int y0 = min(int(fy), Hi - 1);
+    const int y1 = y0 + (y0 < Hi - 1 ? 1 : 0);
+    const float ly = float(fy - y0);
+    const long b = long(v) * Hi * Wi;
+    float a[8], bq[8], cq[8], d[8], y[8];
+    Vec8<T>::load(in, (b + long(y0) * Wi + x0) * C + c, a);
+    Vec8<T>::load(in, (b + long(y0) * Wi + x1) * C + c, bq);
+    Vec8<T>::load(in, (b + long(y1) * Wi + x0) * C + c, cq);
+    Vec8<T>::load(in, (b + long(y1) * Wi + x1) * C + c, d);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) y[k] = (1.f - ly) * ((1.f - lx) * a[k] + lx * bq[k]) + ly * ((1.f - lx) * cq[k] + lx * d[k]);
-  if (addtab) {
-    const float* tp = addtab + (long(oy) * Wo + ox) * C + c;
-    const float4 t0 = *reinterpret_cast<const float4*>(tp), t1 = *reinterpret_cast<const float4*>(tp + 4);
-    y[0] += t0.x; y[1] += t0.y; y[2] += t0.z; y[3] += t0.w; y[4] += t1.x; y[5] += t1.y; y[6] += t1.z; y[7] += t1.w;
-  }
-  if (relu) {
+    for (int k = 0; k < 8; ++k) y[k] = (1.f - ly) * ((1.f - lx) * a[k] + lx * bq[k]) + ly * ((1.f - lx) * cq[k] + lx * d[k]);
+    if (addtab) {
+      const float* tp = addtab + (long(oy) * Wo + ox) * C + c;
+      const float4 t0 = *reinterpret_cast<const float4*>(tp), t1 = *reinterpret_cast<const float4*>(tp + 4);
+      y[0] += t0.x; y[1] += t0.y; y[2] += t0.z; y[3] += t0.w; y[4] += t1.x; y[5] += t1.y; y[6] += t1.z; y[7] += t1.w;
+    }
+    if (relu) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) y[k] = fmaxf(y[k], 0.f);
+      for (int k = 0; k < 8; ++k) y[k] = fmaxf(y[k], 0.f);
+    }
+    Vec8<T>::store(out, (long(row) * Wo + ox) * C + c, y);
   }
-  Vec8<T>::store(out, (long(row) * Wo + ox) * C + c, y);
 }
 
 void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int Wi, int C, void* out, int Hf, int Wf,
@@ -388,10 +399,12 @@ void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int 
   if (C % 8 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(addtab) & 15) == 0) {
     ProfScope ps(ex, "resize_bilinear", 0, (double(V) * Hi * Wi * C + double(total)) * dtype_size(dt) + (addtab ? double(Ho) * Wo * C * 4 : 0));
-    SPLAT_CHECK(long(Wo) * (C / 8) < (1L << 31) && long(V) * Ho < 65536, BAD_ARGUMENT, "resize: grid");
-    dim3 grid(cdiv(long(Wo) * (C / 8), 256), V * Ho);
-    if (dt == F32) hipLaunchKernelGGL(resize8_kernel<float>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
-    else hipLaunchKernelGGL(resize8_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+    const int rows = V * Ho;
+    SPLAT_CHECK(long(Wo) * (C / 8) < (1L << 31) && cdiv(rows, RESIZE_ROWS) < 65536, BAD_ARGUMENT, "resize: grid");
+    const double sy = Hf > 1 ? double(Hi - 1) / double(Hf - 1) : 0.0, sx = Wf > 1 ? double(Wi - 1) / double(Wf - 1) : 0.0;
+    dim3 grid(cdiv(long(Wo) * (C / 8), 256), cdiv(rows, RESIZE_ROWS));
+    if (dt == F32) hipLaunchKernelGGL(resize8_kernel<float>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Ho, Wo, rows, sy, sx, addtab, relu);
+    else hipLaunchKernelGGL(resize8_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Ho, Wo, rows, sy, sx, addtab, relu);
     SPLAT_HIP(hipGetLastError());
     return;
   }
