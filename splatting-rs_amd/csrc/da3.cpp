@@ -104,16 +104,18 @@ void Da3Model::prepare(int V, int H, int W) {
 
 // depthanything3-rs/src/dpt.rs:156-164: exact sizes from the next finer level, the finest
 // fused at twice its size.
-void Da3Model::fusion_chain(const FusionW* chain, void* const pyr[4], const int ph[4], const int pw[4], int V, void* out) {
+void Da3Model::fusion_chain(const FusionW* chain, void* const pyr[4], const int ph[4], const int pw[4], int V, void* out,
+                            const Exec& ex, bool keep) {
   const int F = spec_.head_features;
   const size_t es = dtype_size(dt_);
   void* t3 = ctx_.arena.alloc(size_t(V) * ph[2] * pw[2] * F * es);
-  fusion_block(ctx_, dt_, chain[3], pyr[3], nullptr, V, ph[3], pw[3], ph[2], pw[2], ph[2], pw[2], t3);
+  fusion_block(ctx_, dt_, chain[3], pyr[3], nullptr, V, ph[3], pw[3], ph[2], pw[2], ph[2], pw[2], t3, &ex, keep);
   void* t2 = ctx_.arena.alloc(size_t(V) * ph[1] * pw[1] * F * es);
-  fusion_block(ctx_, dt_, chain[2], t3, pyr[2], V, ph[2], pw[2], ph[1], pw[1], ph[1], pw[1], t2);
+  fusion_block(ctx_, dt_, chain[2], t3, pyr[2], V, ph[2], pw[2], ph[1], pw[1], ph[1], pw[1], t2, &ex, keep);
   void* t1 = ctx_.arena.alloc(size_t(V) * ph[0] * pw[0] * F * es);
-  fusion_block(ctx_, dt_, chain[1], t2, pyr[1], V, ph[1], pw[1], ph[0], pw[0], ph[0], pw[0], t1);
-  fusion_block(ctx_, dt_, chain[0], t1, pyr[0], V, ph[0], pw[0], 2 * ph[0], 2 * pw[0], 2 * ph[0], 2 * pw[0], out);
+  fusion_block(ctx_, dt_, chain[1], t2, pyr[1], V, ph[1], pw[1], ph[0], pw[0], ph[0], pw[0], t1, &ex, keep);
+  fusion_block(ctx_, dt_, chain[0], t1, pyr[0], V, ph[0], pw[0], 2 * ph[0], 2 * pw[0], 2 * ph[0], 2 * pw[0], out, &ex,
+               keep);
 }
 
 void Da3Model::forward(const float* images, int V, int H, int W, const splat_da3_out& out, int32_t* ref_dev,
@@ -228,9 +230,33 @@ void Da3Model::forward(const float* images, int V, int H, int W, const splat_da3
   }
   const int FH = 8 * R, FW = 8 * C;
   {
+    // The ray branch (its fusion chain and output convs) runs on the context's second stream
+    // while the depth branch runs on this one; both only read the pyramid. The ray branch is
+    // enqueued first and keeps all of its arena memory until the join, so nothing the depth
+    // branch allocates (or hands back) overlaps memory the ray branch may still be using.
     const size_t m = ar.mark();
+    const Exec rx = ctx_.fork(ex);
+    void* rays = ar.alloc(size_t(V) * FH * FW * F * es);
+    fusion_chain(ray_chain_, pyr, ph, pw, V, rays, rx, true);
+    const void* r = rays;
+    for (int i = 0; i < 5; ++i) {
+      void* o = ar.alloc(size_t(V) * FH * FW * ray_pre_[i].cout * es);
+      GemmArgs g = conv_args(ray_pre_[i], dt_, r, V, FH, FW, 1, o);
+      if (i == 4) {
+        g.addtab = tb.uv_ray;
+        g.addtab_period = FH * FW;
+      }
+      gemm(rx, g);
+      r = o;
+    }
+    void* ro = ar.alloc(size_t(V) * FH * FW * OUT_HIDDEN * es);
+    gemm(rx, conv_args(ray_out_conv_, dt_, r, V, FH, FW, 1, ro));
+    if (out.ray_logits)
+      pointwise_head(rx, dt_, PW_RAY, ro, long(V) * FH * FW, FH * FW, OUT_HIDDEN, 7, ray_out_w_, ray_out_b_,
+                     out.ray_logits, nullptr, nullptr, nullptr, nullptr);
+
     void* fused = ar.alloc(size_t(V) * FH * FW * F * es);
-    fusion_chain(depth_chain_, pyr, ph, pw, V, fused);
+    fusion_chain(depth_chain_, pyr, ph, pw, V, fused, ex, false);
     void* oc1 = ar.alloc(size_t(V) * FH * FW * (F / 2) * es);
     gemm(ex, conv_args(out_conv1_, dt_, fused, V, FH, FW, 1, oc1));
     void* up = ar.alloc(size_t(V) * H * W * (F / 2) * es);
@@ -241,28 +267,7 @@ void Da3Model::forward(const float* images, int V, int H, int W, const splat_da3
     gemm(ex, g);
     pointwise_head(ex, dt_, PW_DEPTH, o2, long(V) * H * W, H * W, OUT_HIDDEN, 2, oc2_2_w_, oc2_2_b_, out.depth,
                    out.depth_conf, nullptr, nullptr, nullptr);
-    ar.release(m);
-  }
-  {
-    const size_t m = ar.mark();
-    void* rays = ar.alloc(size_t(V) * FH * FW * F * es);
-    fusion_chain(ray_chain_, pyr, ph, pw, V, rays);
-    const void* r = rays;
-    for (int i = 0; i < 5; ++i) {
-      void* o = ar.alloc(size_t(V) * FH * FW * ray_pre_[i].cout * es);
-      GemmArgs g = conv_args(ray_pre_[i], dt_, r, V, FH, FW, 1, o);
-      if (i == 4) {
-        g.addtab = tb.uv_ray;
-        g.addtab_period = FH * FW;
-      }
-      gemm(ex, g);
-      r = o;
-    }
-    void* ro = ar.alloc(size_t(V) * FH * FW * OUT_HIDDEN * es);
-    gemm(ex, conv_args(ray_out_conv_, dt_, r, V, FH, FW, 1, ro));
-    if (out.ray_logits)
-      pointwise_head(ex, dt_, PW_RAY, ro, long(V) * FH * FW, FH * FW, OUT_HIDDEN, 7, ray_out_w_, ray_out_b_,
-                     out.ray_logits, nullptr, nullptr, nullptr, nullptr);
+    ctx_.join(ex);
     ar.release(m);
   }
 

@@ -341,8 +341,8 @@ GemmArgs conv_args(const Conv& c, int dt, const void* in, int V, int Hi, int Wi,
 }
 
 void fusion_block(Context& ctx, int dt, const FusionW& f, const void* x, const void* skip, int V, int h, int w,
-                  int oh_full, int ow_full, int oh, int ow, void* out) {
-  const Exec& ex = ctx.ex;
+                  int oh_full, int ow_full, int oh, int ow, void* out, const Exec* on, bool keep_scratch) {
+  const Exec& ex = on ? *on : ctx.ex;
   const int F = f.u2.c1.cin;
   const size_t bytes = size_t(V) * h * w * F * dtype_size(dt);
   const size_t mark = ctx.arena.mark();
@@ -379,7 +379,7 @@ void fusion_block(Context& ctx, int dt, const FusionW& f, const void* x, const v
   void* z = ctx.arena.alloc(bytes);
   gemm(ex, lin_args(f.out, dt, y, F, V * h * w, z, F));
   resize_bilinear(ex, dt, z, V, h, w, F, out, oh_full, ow_full, oh, ow, nullptr, 0);
-  ctx.arena.release(mark);
+  if (!keep_scratch) ctx.arena.release(mark);
 }
 
 FusionW load_fusion(Loader& L, const std::string& p, int F, bool skip) {
@@ -505,30 +505,60 @@ std::vector<float> uv_table(int channels, int rows, int cols, double aspect) {
 Context::Context(int dev) : device(dev) {
   SPLAT_HIP(hipSetDevice(dev));
   SPLAT_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  SPLAT_HIP(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking));
+  SPLAT_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+  SPLAT_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming));
   ex.stream = stream;
   ex.ws = &ws;
 }
 
+Exec Context::fork(const Exec& on) {
+  Exec b = on;
+  b.stream = aux;
+  b.ws = &ws2;
+  if (!on.dry) {
+    SPLAT_HIP(hipEventRecord(ev_fork, on.stream));
+    SPLAT_HIP(hipStreamWaitEvent(aux, ev_fork, 0));
+  }
+  return b;
+}
+
+void Context::join(const Exec& on) {
+  if (on.dry) return;
+  SPLAT_HIP(hipEventRecord(ev_join, aux));
+  SPLAT_HIP(hipStreamWaitEvent(on.stream, ev_join, 0));
+}
+
 bool Context::reserve_workspace() {
-  if (ws.need <= ws.cap) return false;
-  SPLAT_HIP(hipStreamSynchronize(stream));
-  if (ws.ptr) SPLAT_HIP(hipFree(ws.ptr));
-  ws.ptr = nullptr;
-  ws.cap = 0;
-  SPLAT_HIP(hipMalloc(&ws.ptr, ws.need));
-  ws.cap = ws.need;
-  return true;
+  bool moved = false;
+  for (Workspace* w : {&ws, &ws2}) {
+    if (w->need <= w->cap) continue;
+    SPLAT_HIP(hipStreamSynchronize(stream));
+    SPLAT_HIP(hipStreamSynchronize(aux));
+    if (w->ptr) SPLAT_HIP(hipFree(w->ptr));
+    w->ptr = nullptr;
+    w->cap = 0;
+    SPLAT_HIP(hipMalloc(&w->ptr, w->need));
+    w->cap = w->need;
+    moved = true;
+  }
+  return moved;
 }
 
 Context::~Context() {
   (void)hipSetDevice(device);
   if (stream) (void)hipStreamSynchronize(stream);
+  if (aux) (void)hipStreamSynchronize(aux);
   clear_graphs();
   da3.reset();
   ma.reset();
   for (auto& kv : staging)
     if (kv.second.first) (void)hipFree(kv.second.first);
   if (ws.ptr) (void)hipFree(ws.ptr);
+  if (ws2.ptr) (void)hipFree(ws2.ptr);
+  if (ev_fork) (void)hipEventDestroy(ev_fork);
+  if (ev_join) (void)hipEventDestroy(ev_join);
+  if (aux) (void)hipStreamDestroy(aux);
   if (stream) (void)hipStreamDestroy(stream);
 }
 

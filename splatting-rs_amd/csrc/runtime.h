@@ -143,8 +143,12 @@ GemmArgs lin_args(const Lin& l, int dt, const void* in, long lda, int rows, void
 // resize(out_conv(...)): the 1x1 conv commutes with a bilinear resize.
 struct RcuW { Conv c1, c2; };
 struct FusionW { bool skip = false; RcuW u1, u2; Lin out; };
+// Launches on `on` (default: the context's stream). With keep_scratch its arena scratch stays
+// allocated: a block on a second stream must not hand memory back while later allocations for
+// the first stream may still overlap its kernels.
 void fusion_block(Context& ctx, int dt, const FusionW& f, const void* x, const void* skip, int V, int h, int w,
-                  int oh_full, int ow_full, int oh, int ow, void* out);
+                  int oh_full, int ow_full, int oh, int ow, void* out, const Exec* on = nullptr,
+                  bool keep_scratch = false);
 FusionW load_fusion(Loader& L, const std::string& prefix, int features, bool skip);
 
 // --- models ----------------------------------------------------------------------------------
@@ -176,7 +180,8 @@ class Da3Model {
     float* uv_img = nullptr;   // [H*W, F/2]
     float* uv_ray = nullptr;   // [64*P, F/2]
   };
-  void fusion_chain(const FusionW* chain, void* const pyr[4], const int ph[4], const int pw[4], int V, void* out);
+  void fusion_chain(const FusionW* chain, void* const pyr[4], const int ph[4], const int pw[4], int V, void* out,
+                    const Exec& ex, bool keep_scratch);
 
   Context& ctx_;
   Da3Spec spec_;
@@ -262,8 +267,17 @@ class Context {
   DevicePool pool;
   Arena arena;
   Workspace ws;
-  // Grows `ws` to ws.need (synchronises the stream first; the old buffer may be in use).
-  // True if the buffer moved, which invalidates captured graphs.
+  // A second stream (default priority) for an independent branch of a forward, with its own
+  // split-K workspace. fork() makes it wait for everything enqueued on ex's stream so far and
+  // returns the Exec to launch the branch with; join() makes ex's stream wait for the branch.
+  // Both are event records / waits, so a captured forward captures the branch too.
+  hipStream_t aux = nullptr;
+  Workspace ws2;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  Exec fork(const Exec& on);
+  void join(const Exec& on);
+  // Grows `ws` and `ws2` to their need (synchronises the streams first; the old buffers may be
+  // in use). True if a buffer moved, which invalidates captured graphs.
   bool reserve_workspace();
   std::string last_error;
   bool graphs = false;

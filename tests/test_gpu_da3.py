@@ -131,6 +131,34 @@ def test_da3_c1_fp32(ctx, da3_weights):
 
 
 @pytest.mark.slow
+def test_da3_graph_replay_matches_eager(ctx, da3_weights):
+    """Captured forwards (the ray branch of the head runs on a second stream, forked and joined
+    inside the capture) replay bit-identically to the eager forward, also after a replay on
+    other images, and read their new inputs."""
+    path, w = da3_weights[1.0]
+    images = synth.procedural_images(3, 56, 70, seed=31)
+    other = synth.procedural_images(3, 56, 70, seed=32)
+    report("da3.graph_replay")
+    ctx.load_da3(path, "small", "bf16", specs.REF_SADDLE)
+    eager = ctx.da3_forward_raw(images)
+    eager_other = ctx.da3_forward_raw(other)
+    ctx.set_graphs(True)
+    try:
+        outs = [ctx.da3_forward_raw(images) for _ in range(3)]
+        got_other = ctx.da3_forward_raw(other)
+        again = ctx.da3_forward_raw(images)
+    finally:
+        ctx.set_graphs(False)
+    keys = ("depth", "depth_conf", "ray_logits", "pose_encoding", "camera_tokens")
+    for o in outs + [again]:
+        for k in keys:
+            assert np.array_equal(o[k], eager[k]), k
+        assert o["reference_view"] == eager["reference_view"]
+    for k in keys:
+        assert np.array_equal(got_other[k], eager_other[k]), k
+    assert not np.array_equal(got_other["ray_logits"], eager["ray_logits"])
+
+
 def test_da3_c2_bf16(ctx, da3_weights):
     """6 views 378x504 bf16 (procedural images), LayerScale 1e-5; the
     reference view is pinned to the oracle's choice (its near-tie is tested above)."""
