@@ -654,7 +654,7 @@ void attention(const Exec& ex, const AttnArgs& a) {
   // 4 waves x 32 or 64 queries. Two query sub-tiles per wave (QT = 2) halve the K/V reads per
   // query and win once their grid still gives each CU about two blocks (C5 global 2.46 vs
   // 2.85 ms, C4 encoder 56 vs 62 us); below that the doubled block size leaves CUs idle
-  // (C4 global 261 vs 242 us).
+  // (C4 global 261 vs 242 us; C4 info-sharing per-view blocks, 360 of them, +8 us a launch).
   const long blocks2 = long(cdiv(a.L, 256)) * a.heads * a.seqs;
   const bool qt2 = blocks2 >= 450;
   const long blocks = qt2 ? blocks2 : long(cdiv(a.L, 128)) * a.heads * a.seqs;
