@@ -652,11 +652,12 @@ void attention(const Exec& ex, const AttnArgs& a) {
   // has about two blocks per CU, each slice at least two key tiles (DA3-Small C1: 66 blocks).
   const long gblocks = long(cdiv(a.L, ATTN_WAVES * 32)) * a.heads * a.seqs;
   // 4 waves x 32 or 64 queries. Two query sub-tiles per wave (QT = 2) halve the K/V reads per
-  // query and win once their grid still gives each CU about two blocks (C5 global 2.46 vs
-  // 2.85 ms, C4 encoder 56 vs 62 us); below that the doubled block size leaves CUs idle
-  // (C4 global 261 vs 242 us; C4 info-sharing per-view blocks, 360 of them, +8 us a launch).
+  // query and win once their grid gives each CU about two blocks (C5 global 2.46 vs 2.85 ms);
+  // below that the doubled block size leaves CUs idle (C4 global, 300 such blocks: 261 vs
+  // 242 us; C4 info-sharing per-view, 360: +8 us a launch; C4 encoder per-view, 480: 1.5% of the
+  // attention time).
   const long blocks2 = long(cdiv(a.L, 256)) * a.heads * a.seqs;
-  const bool qt2 = blocks2 >= 450;
+  const bool qt2 = blocks2 >= 500;
   const long blocks = qt2 ? blocks2 : long(cdiv(a.L, 128)) * a.heads * a.seqs;
   const int ntiles = cdiv(a.L, 64);
   const int S = bf_fast ? (a.L >= 4096 ? attn_splits(blocks, ntiles) : 1)
