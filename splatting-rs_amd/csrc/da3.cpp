@@ -200,13 +200,17 @@ void Da3Model::forward(const float* images, int V, int H, int W, const splat_da3
   const int ph[4] = {4 * R, 2 * R, R, R2}, pw[4] = {4 * C, 2 * C, C, C2};
   void* pyr[4];
   for (int k = 0; k < 4; ++k) pyr[k] = ar.alloc(size_t(V) * ph[k] * pw[k] * F * es);
-  for (int k = 0; k < 4; ++k) {
+  // The four hook adapters are independent until the fusion chains: levels 2 and 3 run on the
+  // context's second stream while 0 and 1 run here (their convolutions each leave most CUs
+  // idle). The second stream's levels are enqueued first and keep their arena memory until the
+  // join.
+  auto adapter = [&](int k, const Exec& e, bool keep) {
     const size_t m = ar.mark();
     void* pk = ar.alloc(size_t(V) * P * c[k] * es);
     GemmArgs g = lin_args(proj_[k], dt_, hook[k], 2 * d, V * P, pk, c[k]);
     g.addtab = tb.uv[k];
     g.addtab_period = P;
-    gemm(ex, g);
+    gemm(e, g);
     const void* r = pk;
     if (k == 0 || k == 1) {
       const ConvT& ct = k == 0 ? rs0_ : rs1_;
@@ -218,15 +222,25 @@ void Da3Model::forward(const float* images, int V, int H, int W, const splat_da3
       u.ct_R = R;
       u.ct_C = C;
       u.ct_Cout = c[k];
-      gemm(ex, u);
+      gemm(e, u);
       r = up;
     } else if (k == 3) {
       void* dn = ar.alloc(size_t(V) * R2 * C2 * c[k] * es);
-      gemm(ex, conv_args(rs3_, dt_, pk, V, R, C, 2, dn));
+      gemm(e, conv_args(rs3_, dt_, pk, V, R, C, 2, dn));
       r = dn;
     }
-    gemm(ex, conv_args(rn_[k], dt_, r, V, ph[k], pw[k], 1, pyr[k]));
-    ar.release(m);
+    gemm(e, conv_args(rn_[k], dt_, r, V, ph[k], pw[k], 1, pyr[k]));
+    if (!keep) ar.release(m);
+  };
+  {
+    const size_t madapt = ar.mark();
+    const Exec ax = ctx_.fork(ex);
+    adapter(3, ax, true);
+    adapter(2, ax, true);
+    adapter(0, ex, false);
+    adapter(1, ex, false);
+    ctx_.join(ex);
+    ar.release(madapt);
   }
   const int FH = 8 * R, FW = 8 * C;
   {
