@@ -33,6 +33,9 @@ GEMM_CASES = [
     (100, 256, 4096, 0),
     (777, 64, 2048, 2),
     (300, 1001, 2048, 1),
+    # DA3-Small C1 shapes (1297 rows, K = 384): few tiles, K too short to split
+    (1297, 384, 384, 0),
+    (1297, 1536, 384, 2),
 ]
 
 
