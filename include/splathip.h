@@ -7,8 +7,11 @@
  *
  * Threading: a context is not thread-safe; the caller serialises calls on it (the reference's
  * model is used from one thread, depthanything3-rs/src/pipeline.rs:58-73). Contexts are
- * independent; each owns one HIP stream on its device, the loaded weights and an
- * activation arena that grows to the largest input seen.
+ * independent; each owns a HIP stream on its device (splat_stream), the loaded weights and an
+ * activation arena that grows to the largest input seen. A forward may run independent
+ * branches on a second, internal stream of the context; every branch waits for the work
+ * enqueued on splat_stream before it and splat_stream waits for the branch before anything
+ * enqueued after it, so ordering against splat_stream orders the whole forward.
  *
  * Tensors: images are [V, 3, H, W] float32, ImageNet-normalised, H and W multiples of 14.
  * Host-pointer entry points copy inputs in and outputs out and synchronise before
