@@ -867,7 +867,10 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p, in
 
 constexpr int GEMM_CUS = 256;  // MI355X compute units: one "round" of resident blocks per CU slot
 
-template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 128 / sizeof(T), int MINB = 1>
+// TAP_ONLY: an instantiation that serves per-tap convolutions only (the 32-element k-tiles for
+// maps whose Cin is a multiple of 32 but not of 64).
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 128 / sizeof(T), int MINB = 1,
+          bool TAP_ONLY = false>
 static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   static_assert(MINB == 1 || MINB * STAGES * (BM + BN) * BK * sizeof(T) <= 160 * 1024, "LDS of MINB blocks per CU");
   const int tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
@@ -887,15 +890,18 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   const bool tap = a.amode == A_CONV && a.Cin % BK == 0 && a.ks * a.ks <= 32;
   SPLAT_CHECK(a.amode == A_ROWS || tap || !a.relu_in, BAD_ARGUMENT,
               "gemm: ReLU-on-load needs a convolution whose Cin is a multiple of the k-tile");
+  if (TAP_ONLY) SPLAT_CHECK(tap && epi != EPI_HEAD, BAD_ARGUMENT, "gemm: 32-element k-tiles serve per-tap convs only");
   if (epi == EPI_HEAD) {  // the fused MapAnything head: one tile spans the 128 channels
     SPLAT_CHECK(tap && !a.relu_in && a.N == BN && a.act == ACT_RELU && S == 1, BAD_ARGUMENT, "gemm: fused head");
-    if constexpr (BN == 128 && sizeof(T) == 2) SPLAT_GO(A_CONV_TAP, false, EPI_HEAD);
+    if constexpr (BN == 128 && sizeof(T) == 2 && !TAP_ONLY) SPLAT_GO(A_CONV_TAP, false, EPI_HEAD);
     else SPLAT_CHECK(false, BAD_ARGUMENT, "gemm: fused head needs a bf16 128-column tile");
   } else if (a.amode == A_ROWS) {
-    if (epi == EPI_PART) SPLAT_GO(A_ROWS, false, EPI_PART);
-    else if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
-    else if (epi == EPI_RES) SPLAT_GO(A_ROWS, false, EPI_RES);
-    else SPLAT_GO(A_ROWS, false, EPI_FULL);
+    if constexpr (!TAP_ONLY) {
+      if (epi == EPI_PART) SPLAT_GO(A_ROWS, false, EPI_PART);
+      else if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
+      else if (epi == EPI_RES) SPLAT_GO(A_ROWS, false, EPI_RES);
+      else SPLAT_GO(A_ROWS, false, EPI_FULL);
+    }
   } else if (tap) {
     if (epi == EPI_PART) {
       if (a.relu_in) SPLAT_GO(A_CONV_TAP, true, EPI_PART);
@@ -910,9 +916,11 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
       else SPLAT_GO(A_CONV_TAP, false, EPI_FULL);
     }
   } else {
-    if (epi == EPI_PART) SPLAT_GO(A_CONV, false, EPI_PART);
-    else if (epi == EPI_BIAS) SPLAT_GO(A_CONV, false, EPI_BIAS);
-    else SPLAT_GO(A_CONV, false, EPI_FULL);
+    if constexpr (!TAP_ONLY) {
+      if (epi == EPI_PART) SPLAT_GO(A_CONV, false, EPI_PART);
+      else if (epi == EPI_BIAS) SPLAT_GO(A_CONV, false, EPI_BIAS);
+      else SPLAT_GO(A_CONV, false, EPI_FULL);
+    }
   }
 #undef SPLAT_GO
   SPLAT_HIP(hipGetLastError());
@@ -1035,6 +1043,18 @@ static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
   const BfCfg c = pick_bf16(a);
   int S = split_factor(a, c);
   if (S > 1 && !(ex.ws && ex.ws->ptr && ex.ws->cap >= split_bytes(a, S))) S = 1;
+  // Convolutions whose Cin is a multiple of 32 but not of 64 (96-channel maps): 32-element
+  // k-tiles keep them on the per-tap path for the tiles whose rows split into 16-row loads
+  // (256x256 with a third stage, so that the epilogue slabs fit the ring)
+  if (a.amode == A_CONV && a.Cin % 64 != 0 && a.Cin % 32 == 0 && a.ks * a.ks <= 32 && !a.hw3) {
+    switch (c) {
+      case CFG_128x64: return launch_mfma<bf16, 128, 64, 2, 2, 2, 32, 1, true>(ex, a, S);
+      case CFG_256x256: return launch_mfma<bf16, 256, 256, 2, 4, 3, 32, 1, true>(ex, a, S);
+      case CFG_256x128: return launch_mfma<bf16, 256, 128, 4, 2, 3, 32, 1, true>(ex, a, S);
+      case CFG_128x128: return launch_mfma<bf16, 128, 128, 2, 2, 4, 32, 1, true>(ex, a, S);
+      default: break;  // 320- and 192-row and 32-column tiles: the per-lane path
+    }
+  }
   switch (c) {
     case CFG_128x32: return launch_mfma<bf16, 128, 32, 4, 1, 2>(ex, a, S);
     case CFG_128x64: return launch_mfma<bf16, 128, 64, 2, 2, 2>(ex, a, S);

@@ -151,6 +151,11 @@ CONV_CASES = [
     # split-K: the DPT head's coarsest level (M = 1596, K = 6912) and a narrow conv
     (6, 19, 14, 768, 256, 3, 1, 0, 0, True),
     (2, 9, 7, 512, 64, 3, 1, 1, 1, False),
+    # Cin a multiple of 32 but not 64: per-tap path on 32-element k-tiles (bf16), bias; ReLU-on-load
+    # + residual; split-K (K = 1440)
+    (2, 16, 12, 96, 64, 3, 1, 0, 0, False),
+    (1, 28, 37, 96, 256, 3, 1, 1, 1, True),
+    (1, 9, 7, 160, 64, 3, 1, 0, 0, False),
     # 128 output channels over >= 768 tiles of 192 rows: the two-blocks-per-CU tile (bf16),
     # bias + ReLU epilogue, then ReLU-on-load with a residual (the full epilogue)
     (3, 224, 224, 64, 128, 3, 1, 0, 1, False),
