@@ -45,7 +45,11 @@ typedef enum splat_status {
   SPLAT_NOT_LOADED = 8
 } splat_status;
 
-typedef enum splat_dtype { SPLAT_F32 = 0, SPLAT_BF16 = 1, SPLAT_F16 = 2 /* computed as bf16 */ } splat_dtype;
+/* The model dtype of the loaders (candle's DType, depthanything3-rs/src/main.rs:60-61,
+ * mapanything-rs/src/main.rs:59-60). SPLAT_F16 is declared for the reference's --precision f16
+ * but not implemented: the loaders return SPLAT_BAD_ARGUMENT for it rather than computing in
+ * another precision than the one asked for. */
+typedef enum splat_dtype { SPLAT_F32 = 0, SPLAT_BF16 = 1, SPLAT_F16 = 2 } splat_dtype;
 
 /* depthanything3-rs/src/variant.rs:17-23 */
 typedef enum splat_da3_variant { SPLAT_DA3_SMALL = 0, SPLAT_DA3_BASE = 1, SPLAT_DA3_LARGE = 2, SPLAT_DA3_GIANT = 3 } splat_da3_variant;
@@ -64,6 +68,14 @@ typedef void (*splat_progress_fn)(int stage, int block, void* user);
  * after backbone / encoder / info-sharing block `block` (blocks numbered across stages).
  * Forces a synchronisation per block. */
 typedef void (*splat_tap_fn)(int block, const float* hidden, int rows, int dim, void* user);
+
+/* Debug tap of a block's two residual branches before their LayerScale: branch 0 is the
+ * attention branch proj(attn(...)) + bias, branch 1 the feed-forward output fc2(...) + bias
+ * (depthanything3-rs/src/vit_block.rs:163-166, mapanything-rs/src/vit_block.rs:103-106), as
+ * float32 [rows, dim] host memory valid during the call; rows is the block's own row count
+ * (a per-view MapAnything info block leaves out the scale token). Each tap recomputes the
+ * branch's last GEMM without the LayerScale and residual epilogue and synchronises. */
+typedef void (*splat_branch_tap_fn)(int block, int branch, const float* out, int rows, int dim, void* user);
 
 /* MapAnything widths. The reference hard-codes them (mapanything-rs/src/dinov2.rs:8-17,
  * info_sharing.rs:12-14, dpt.rs:10-14, heads.rs:9-15); ffn: 0 = GELU MLP, 1 = SwiGLU. */
@@ -126,10 +138,14 @@ const char* splat_last_error(const splat_ctx* ctx);
 void* splat_stream(splat_ctx* ctx);
 int splat_synchronize(splat_ctx* ctx);
 /* 1 = capture each forward shape into a HIP graph on first use and replay it (default 0).
- * Ignored while progress callbacks or debug taps are set. */
+ * Ignored while progress callbacks, debug taps or branch taps are set. */
 int splat_set_graphs(splat_ctx* ctx, int enable);
 /* Per-block residual taps (NULL to disable); replaces nothing in the reference: a test hook. */
 int splat_set_debug_taps(splat_ctx* ctx, splat_tap_fn fn, void* user);
+/* Per-block branch taps (NULL to disable), a test hook like splat_set_debug_taps: the reference
+ * has no counterpart; they make a block's arithmetic visible where LayerScale 1e-5 leaves the
+ * residual stream nearly unchanged. */
+int splat_set_branch_taps(splat_ctx* ctx, splat_branch_tap_fn fn, void* user);
 
 /* mapanything-rs/src/image_input.rs:195-216 (to_model_input, used by both crates' preprocess):
  * host RGBA u8 [V, H, W, 4] (already resized and cropped) -> device images [V, 3, H, W] f32,

@@ -24,8 +24,9 @@ MIN_SCALE = 1e-8        # mapanything-rs/src/heads.rs:17
 RAY_WIDTHS = (3 * 14 * 14, 768, 1024)  # mapanything-rs/src/ray_encoder.rs:11-12
 
 
-def encoder_forward(p, spec, images, taps=None):
-    """mapanything-rs/src/dinov2.rs:129-145, all views batched (each view is independent)."""
+def encoder_forward(p, spec, images, taps=None, branch_taps=None):
+    """mapanything-rs/src/dinov2.rs:129-145, all views batched (each view is independent).
+    branch_taps: per block, the [attention, feed-forward] branch outputs before LayerScale."""
     V, _, H, W = images.shape
     R, Cc = H // C.PATCH, W // C.PATCH
     e = "encoder.model"
@@ -33,14 +34,19 @@ def encoder_forward(p, spec, images, taps=None):
     pos = C.positional_embedding(p[e + ".pos_embed"], R, Cc).to(images.dtype)
     xs = torch.cat([p[e + ".cls_token"].expand(V, 1, spec.enc_dim), patches], 1) + pos
     for i in range(spec.enc_depth):
-        xs = C.vit_block(xs, p, f"{e}.blocks.{i}", spec.enc_ffn == 1, LN_EPS)
+        bt = [] if branch_taps is not None else None
+        xs = C.vit_block(xs, p, f"{e}.blocks.{i}", spec.enc_ffn == 1, LN_EPS, taps=bt)
         if taps is not None:
             taps.append(xs.clone())
+        if branch_taps is not None:
+            branch_taps.append([t[1].clone() for t in bt])
     return xs
 
 
-def info_sharing_forward(p, spec, patches, classes, taps=None):
-    """mapanything-rs/src/info_sharing.rs:50-102. patches [V, P, d], classes [V, 1, d]."""
+def info_sharing_forward(p, spec, patches, classes, taps=None, branch_taps=None):
+    """mapanything-rs/src/info_sharing.rs:50-102. patches [V, P, d], classes [V, 1, d].
+    branch_taps: per block, the [attention, feed-forward] branch outputs before LayerScale
+    (a per-view block's cover the V*n view tokens only; the scale token waits)."""
     V, P, d = patches.shape
     n = P + 1
     q = "info_sharing"
@@ -50,14 +56,17 @@ def info_sharing_forward(p, spec, patches, classes, taps=None):
     stored = []
     for i in range(spec.info_depth):
         name = f"{q}.self_attention_blocks.{i}"
+        bt = [] if branch_taps is not None else None
         if i % 2 == 0:
-            xs = C.vit_block(xs, p, name, spec.info_ffn == 1, LN_EPS)
+            xs = C.vit_block(xs, p, name, spec.info_ffn == 1, LN_EPS, taps=bt)
         else:
             per_view = xs[:, :V * n].reshape(V, n, d)
-            att = C.vit_block(per_view, p, name, spec.info_ffn == 1, LN_EPS).reshape(1, V * n, d)
+            att = C.vit_block(per_view, p, name, spec.info_ffn == 1, LN_EPS, taps=bt).reshape(1, V * n, d)
             xs = torch.cat([att, xs[:, V * n:]], 1)
         if taps is not None:
             taps.append(xs.clone())
+        if branch_taps is not None:
+            branch_taps.append([t[1].clone() for t in bt])
         if i in spec.hooks:
             stored.append(C.layer_norm(xs, p[q + ".norm.weight"], p[q + ".norm.bias"], LN_EPS))
     per_view = [[s[0, v * n: v * n + P] for s in stored] for v in range(V)]
@@ -173,7 +182,7 @@ def ray_encoder(p, rays: torch.Tensor) -> torch.Tensor:
 
 
 def forward(weights, spec, images, dtype=torch.float32, encoder_only=False, taps=None, info_taps=None,
-            intrinsics=None) -> dict:
+            intrinsics=None, branch_taps=None, info_branch_taps=None) -> dict:
     """mapanything-rs/src/model.rs:86-144. intrinsics: None, or one entry per view, each None
     (unknown camera, model.rs:103) or (fx, fy, cx, cy) (known: the ray encoder's features are
     added to the image patches before the fusion norm, model.rs:97-102)."""
@@ -183,7 +192,7 @@ def forward(weights, spec, images, dtype=torch.float32, encoder_only=False, taps
     R, Cc = H // C.PATCH, W // C.PATCH
     P = R * Cc
     with torch.no_grad():
-        tokens = encoder_forward(p, spec, x, taps)
+        tokens = encoder_forward(p, spec, x, taps, branch_taps)
         if encoder_only:
             return {"encoder_tokens": tokens.float()}
         patches = tokens[:, 1:]
@@ -201,7 +210,7 @@ def forward(weights, spec, images, dtype=torch.float32, encoder_only=False, taps
         if spec.has_proj:
             info_patches = C.linear(fused, p, "info_sharing.proj_embed")
             info_classes = C.linear(classes, p, "info_sharing.proj_embed")
-        per_view, scale_tok = info_sharing_forward(p, spec, info_patches, info_classes, info_taps)
+        per_view, scale_tok = info_sharing_forward(p, spec, info_patches, info_classes, info_taps, info_branch_taps)
         scale = scale_head(p, scale_tok[None])[0]
         hooks = [fused] + [torch.stack([pv[k] for pv in per_view]) for k in range(3)]
         raw = dpt_forward(p, spec, hooks, R, Cc).float()

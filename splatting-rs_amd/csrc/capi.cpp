@@ -37,7 +37,9 @@ int guard(Context* ctx, F&& fn) {
 }
 
 int model_dtype(int dtype) {
-  SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16 || dtype == SPLAT_F16, BAD_ARGUMENT, "unknown dtype");
+  SPLAT_CHECK(dtype != SPLAT_F16, BAD_ARGUMENT,
+              "dtype SPLAT_F16 is not implemented (use SPLAT_BF16 or SPLAT_F32; no silent narrowing to bf16)");
+  SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "unknown dtype");
   return dtype == SPLAT_F32 ? F32 : BF16;
 }
 
@@ -50,7 +52,7 @@ void check_images(const float* images, int V, int H, int W) {
 
 void* staging(Context* ctx, int slot, size_t bytes) { return ctx->staging_buffer(slot, bytes); }
 
-bool use_graphs(Context* ctx) { return ctx->graphs && !ctx->hooks.tap && !ctx->hooks.progress && !ctx->ex.prof; }
+bool use_graphs(Context* ctx) { return ctx->graphs && !ctx->hooks.any() && !ctx->ex.prof; }
 
 void da3_device(Context* ctx, const float* images, int V, int H, int W, const splat_da3_out& out, int32_t* ref) {
   SPLAT_CHECK(ctx->da3 != nullptr, NOT_LOADED, "no Depth Anything 3 model loaded");
@@ -167,6 +169,13 @@ int splat_set_debug_taps(splat_ctx* ctx, splat_tap_fn fn, void* user) {
   return guard(C(ctx), [&] {
     C(ctx)->hooks.tap = fn;
     C(ctx)->hooks.tap_user = user;
+  });
+}
+
+int splat_set_branch_taps(splat_ctx* ctx, splat_branch_tap_fn fn, void* user) {
+  return guard(C(ctx), [&] {
+    C(ctx)->hooks.branch_tap = fn;
+    C(ctx)->hooks.branch_user = user;
   });
 }
 

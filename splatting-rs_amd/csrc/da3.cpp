@@ -174,9 +174,9 @@ void Da3Model::forward(const float* images, int V, int H, int W, const splat_da3
     const int rope = i >= spec_.alt_start ? (across ? 2 : 1) : 0;
     float* dst = cur == within ? (cur == X0 ? X1 : X0) : cur;
     if (across) {
-      block_forward(ctx_, blocks_[i], dt_, cur, dst, T, 1, T, s, rope, n, C, tb.rope, tb.npos);
+      block_forward(ctx_, blocks_[i], dt_, cur, dst, T, 1, T, s, rope, n, C, tb.rope, tb.npos, i);
     } else {
-      block_forward(ctx_, blocks_[i], dt_, cur, dst, T, V, n, s, rope, n, C, tb.rope, tb.npos);
+      block_forward(ctx_, blocks_[i], dt_, cur, dst, T, V, n, s, rope, n, C, tb.rope, tb.npos, i);
       within = dst;
     }
     cur = dst;

@@ -149,7 +149,7 @@ void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_o
     block_scratch(ctx_, s, dt_, Te, e, spec_.enc_hidden, spec_.enc_ffn == 1);
     for (int i = 0; i < spec_.enc_depth; ++i) {
       progress(SPLAT_STAGE_BLOCK, i);
-      block_forward(ctx_, enc_[i], dt_, xe, xe, Te, V, n, s, 0, n, C, nullptr, 0);
+      block_forward(ctx_, enc_[i], dt_, xe, xe, Te, V, n, s, 0, n, C, nullptr, 0, i);
       tap(i, xe, Te, e);
     }
     ar.release(m);
@@ -241,8 +241,8 @@ void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_o
     int stored = 0;
     for (int i = 0; i < spec_.info_depth; ++i) {
       progress(SPLAT_STAGE_BLOCK, spec_.enc_depth + i);
-      if (i % 2 == 0) block_forward(ctx_, info_[i], dt_, xi, xi, Ti, 1, int(Ti), s, 0, n, C, nullptr, 0);
-      else block_forward(ctx_, info_[i], dt_, xi, xi, long(V) * n, V, n, s, 0, n, C, nullptr, 0);
+      if (i % 2 == 0) block_forward(ctx_, info_[i], dt_, xi, xi, Ti, 1, int(Ti), s, 0, n, C, nullptr, 0, spec_.enc_depth + i);
+      else block_forward(ctx_, info_[i], dt_, xi, xi, long(V) * n, V, n, s, 0, n, C, nullptr, 0, spec_.enc_depth + i);
       tap(spec_.enc_depth + i, xi, Ti, d);
       if (stored < 3 && i == spec_.hooks[stored]) {
         layer_norm(ex, F32, xi, d, dt_, hk[stored], d, V * P, d, info_norm_.w, info_norm_.b, LN_EPS, P, n, 0);

@@ -205,9 +205,28 @@ void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, in
 }
 
 void block_forward(Context& ctx, const Block& b, int dt, const float* in, float* out, long rows, int seqs, int L,
-                   BlockScratch& s, int rope, int n, int cols, const float* rope_table, int npos) {
+                   BlockScratch& s, int rope, int n, int cols, const float* rope_table, int npos, int block) {
   const Exec& ex = ctx.ex;
   const int d = b.dim;
+  // Branch tap: the branch's last GEMM again, bias only (no LayerScale, no residual), into an
+  // fp32 temporary that is copied to the host (the dry run sizes the temporary too).
+  auto branch_tap = [&](int which, const Lin& l, const void* A, long lda, int K) {
+    const Hooks& hk = ctx.hooks;
+    if (!hk.branch_tap) return;
+    const size_t m = ctx.arena.mark();
+    float* y = ctx.arena.alloc_t<float>(size_t(rows) * d);
+    GemmArgs g = lin_args(l, dt, A, lda, int(rows), y, d);
+    g.K = K;
+    g.out_f32 = 1;
+    gemm(ex, g);
+    if (!ex.dry) {
+      std::vector<float> host(size_t(rows) * d);
+      SPLAT_HIP(hipMemcpyAsync(host.data(), y, host.size() * 4, hipMemcpyDeviceToHost, ex.stream));
+      SPLAT_HIP(hipStreamSynchronize(ex.stream));
+      hk.branch_tap(block, which, host.data(), int(rows), d, hk.branch_user);
+    }
+    ctx.arena.release(m);
+  };
   // norm1 -> qkv
   layer_norm(ex, F32, in, d, dt, s.h, d, int(rows), d, b.n1.w, b.n1.b, 1e-6f);
   GemmArgs g;
@@ -241,6 +260,7 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
   a.seqs = seqs;
   a.seq_stride = L;
   attention(ex, a);
+  branch_tap(0, b.proj, s.att, d, d);
   // out = in + ls1 * proj(att)
   GemmArgs p;
   p.dt = dt;
@@ -284,6 +304,7 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
     f1.ldc = b.hidden;
     gemm(ex, f1);
   }
+  branch_tap(1, b.fc2, s.mid, b.hidden, b.hidden);
   GemmArgs f2;
   f2.dt = dt;
   f2.M = int(rows);

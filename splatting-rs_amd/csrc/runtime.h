@@ -111,6 +111,9 @@ struct Hooks {
   void* progress_user = nullptr;
   splat_tap_fn tap = nullptr;
   void* tap_user = nullptr;
+  splat_branch_tap_fn branch_tap = nullptr;
+  void* branch_user = nullptr;
+  bool any() const { return progress || tap || branch_tap; }
 };
 
 // Scratch buffers of one transformer stack, sized for its largest block.
@@ -127,9 +130,10 @@ class Context;
 void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, int hidden, bool swiglu);
 // One pre-norm transformer block over `rows` rows of `in` (fp32 [rows, dim]) into `out`
 // (may equal `in`): sequences of L rows each (`seqs` of them); rope: 0 none, 1 within view,
-// 2 across views (positions from n tokens per view and `cols` patch columns).
+// 2 across views (positions from n tokens per view and `cols` patch columns). `block` numbers
+// the block for the context's branch taps.
 void block_forward(Context& ctx, const Block& b, int dt, const float* in, float* out, long rows, int seqs, int L,
-                   BlockScratch& s, int rope, int n, int cols, const float* rope_table, int npos);
+                   BlockScratch& s, int rope, int n, int cols, const float* rope_table, int npos, int block);
 
 // GEMM arguments of a convolution on an NHWC map [V, Hi, Wi, cin]: ks == 1 -> plain rows,
 // ks == 3 -> implicit im2col with padding 1. The caller adds epilogue fields.

@@ -70,6 +70,7 @@ class KernelStatC(C.Structure):
 
 PROGRESS_FN = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_void_p)
 TAP_FN = C.CFUNCTYPE(None, C.c_int, C.POINTER(C.c_float), C.c_int, C.c_int, C.c_void_p)
+BRANCH_TAP_FN = C.CFUNCTYPE(None, C.c_int, C.c_int, C.POINTER(C.c_float), C.c_int, C.c_int, C.c_void_p)
 
 # Every symbol the two public headers declare, with its ctypes signature.
 SIGNATURES = {
@@ -80,6 +81,7 @@ SIGNATURES = {
     "splat_synchronize": (C.c_int, [C.c_void_p]),
     "splat_set_graphs": (C.c_int, [C.c_void_p, C.c_int]),
     "splat_set_debug_taps": (C.c_int, [C.c_void_p, TAP_FN, C.c_void_p]),
+    "splat_set_branch_taps": (C.c_int, [C.c_void_p, BRANCH_TAP_FN, C.c_void_p]),
     "splat_load_da3": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int, C.c_int, C.c_int]),
     "splat_load_da3_bytes": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int]),
     "splat_da3_forward_raw": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, PROGRESS_FN, C.c_void_p,
@@ -184,6 +186,18 @@ class Context:
         cb = TAP_FN(tap)
         self._callbacks.append(cb)
         self.check(self._lib.splat_set_debug_taps(self.handle, cb, None))
+
+    def set_branch_taps(self, fn):
+        """fn(block, branch, ndarray [rows, dim]) per block and branch (0 attention, 1
+        feed-forward; the branch output before its LayerScale), or None."""
+        if fn is None:
+            self.check(self._lib.splat_set_branch_taps(self.handle, BRANCH_TAP_FN(), None))
+            return
+        def tap(block, branch, ptr, rows, dim, user):
+            fn(block, branch, np.ctypeslib.as_array(ptr, shape=(rows, dim)).copy())
+        cb = BRANCH_TAP_FN(tap)
+        self._callbacks.append(cb)
+        self.check(self._lib.splat_set_branch_taps(self.handle, cb, None))
 
     # --- Depth Anything 3 -------------------------------------------------------------------
     def load_da3(self, path: str, variant: str = "small", dtype: str = "f32", strategy: int = specs.REF_SADDLE):

@@ -145,6 +145,10 @@ def test_ma_views_equivariance(ctx, ma_weights):
 
 def test_ma_errors(ctx, ma_weights):
     path, w, spec = ma_weights[("tiny", 1e-5)]
+    # the reference CLI's default f16 is refused rather than computed as bf16
+    with pytest.raises(splathip.SplatError) as e:
+        ctx.load_mapanything(path, spec, "f16")
+    assert e.value.code == splathip.BAD_ARGUMENT
     ctx.load_mapanything(path, spec, "f32")
     with pytest.raises(splathip.SplatError) as e:
         ctx.ma_forward(np.zeros((1, 3, 56, 69), np.float32))
