@@ -22,6 +22,17 @@ int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, co
  * reading q, k and v from a [S*L, 3*heads*64] qkv matrix (q | k | v column blocks). */
 int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads);
 
+/* splat_kernel_attention that allocates nothing. It has no counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same kernels and key-slice plan; the fp32 partials
+ * of a key-sliced launch (long sequences) live in a statically allocated scratch of 64 MiB per
+ * GPU (ATTN_SCRATCH_BYTES, held by every GPU the library runs on until the process ends)
+ * instead of the context's workspace. A launch whose partials need more than that returns
+ * SPLAT_BAD_ARGUMENT (e.g. 24889 tokens x 12 heads needs 236 MB; 6223 x 12 needs 59 MB). Every
+ * call on one GPU shares that scratch, which keeps the last call's contents: calls that
+ * overlap on one GPU (other contexts or streams) race. Profiling records are not taken. */
+int splat_kernel_attention_noalloc(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads);
+
 /* Convolution (zero padding ks/2) on NHWC maps as an implicit GEMM:
  * out[V, Ho, Wo, Cout] = act(conv(relu_in ? relu(in) : in, w) + bias) + res, with
  * w [Cout, ldw] holding k = (ky*ks + kx)*Cin + ci (candle/PyTorch weight [Cout, Cin, ks, ks]

@@ -13,9 +13,37 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 namespace splat {
+
+// Device-resident scratch for the key-slice partials of attention launches that must not
+// allocate (splat_kernel_attention_noalloc): one copy per GPU, held until the process ends.
+// Host code never passes `scratch` itself to a kernel (on the host the name is only a stand-in
+// for the symbol): attention_scratch() looks up each device's address once, with that device
+// current, and callers use that address.
+static __device__ __align__(256) char scratch[ATTN_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_addr[ATTN_SCRATCH_DEVICES] = {};
+}  // namespace
+
+void* attention_scratch(int device) {
+  SPLAT_CHECK(device >= 0 && device < ATTN_SCRATCH_DEVICES, BAD_ARGUMENT, "attention scratch: device index");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[device]) {
+    int cur = -1;
+    SPLAT_HIP(hipGetDevice(&cur));
+    SPLAT_CHECK(cur == device, BAD_ARGUMENT, "attention scratch: the device must be current");
+    void* p = nullptr;
+    SPLAT_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    SPLAT_CHECK(p != nullptr, HIP_ERROR, "attention scratch: no device address");
+    g_scratch_addr[device] = p;
+  }
+  return g_scratch_addr[device];
+}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

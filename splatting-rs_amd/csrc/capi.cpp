@@ -118,6 +118,23 @@ void load_da3(Context* ctx, SafeTensors& st, int variant, int dtype, int strateg
   ctx->da3 = std::make_unique<Da3Model>(*ctx, st, variant, dt, strategy);
 }
 
+AttnArgs attention_args(int dtype, const void* qkv, void* out, int S, int L, int heads) {
+  SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
+  AttnArgs a;
+  a.dt = dtype == SPLAT_F32 ? F32 : BF16;
+  const size_t es = dtype_size(a.dt);
+  a.q = qkv;
+  a.k = static_cast<const char*>(qkv) + size_t(heads) * 64 * es;
+  a.v = static_cast<const char*>(qkv) + size_t(heads) * 128 * es;
+  a.ld = 3L * heads * 64;
+  a.o = out;
+  a.ldo = long(heads) * 64;
+  a.L = L;
+  a.heads = heads;
+  a.seqs = S;
+  a.seq_stride = L;
+  return a;
+}
 template <typename T>
 void d2h(Context* ctx, T* host, const void* dev, size_t count) {
   if (host) SPLAT_HIP(hipMemcpyAsync(host, dev, count * sizeof(T), hipMemcpyDeviceToHost, ctx->stream));
@@ -356,22 +373,33 @@ int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, co
   });
 }
 
+int splat_kernel_attention_noalloc(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads) {
+  return guard(C(ctx), [&] {
+    Context* c = C(ctx);
+    const AttnArgs a = attention_args(dtype, qkv, out, S, L, heads);
+    // the same kernels and key-slice plan as splat_kernel_attention, with the partials in this
+    // device's static scratch instead of the context's workspace; no profiling records (their
+    // events are created per launch)
+    SPLAT_CHECK(c->attn_scratch != nullptr, HIP_ERROR, "attention scratch: not set up");
+    Workspace ws;
+    ws.ptr = c->attn_scratch;
+    ws.cap = ATTN_SCRATCH_BYTES;
+    Exec e = c->ex;
+    e.ws = &ws;
+    e.prof = nullptr;
+    Exec dry = e;
+    dry.dry = true;
+    attention(dry, a);  // sizes the partials of the launch's key slices in ws.need
+    SPLAT_CHECK(ws.need <= ws.cap, BAD_ARGUMENT,
+                "attention: the key-slice partials of this launch need " + std::to_string(ws.need) +
+                    " bytes of scratch; the allocation-free entry point has " + std::to_string(ws.cap));
+    attention(e, a);
+  });
+}
+
 int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads) {
   return guard(C(ctx), [&] {
-    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
-    AttnArgs a;
-    a.dt = dtype == SPLAT_F32 ? F32 : BF16;
-    const size_t es = dtype_size(a.dt);
-    a.q = qkv;
-    a.k = static_cast<const char*>(qkv) + size_t(heads) * 64 * es;
-    a.v = static_cast<const char*>(qkv) + size_t(heads) * 128 * es;
-    a.ld = 3L * heads * 64;
-    a.o = out;
-    a.ldo = long(heads) * 64;
-    a.L = L;
-    a.heads = heads;
-    a.seqs = S;
-    a.seq_stride = L;
+    const AttnArgs a = attention_args(dtype, qkv, out, S, L, heads);
     Context* c = C(ctx);
     Exec dry = c->ex;  // a dry pass sizes the key-split partials first
     dry.dry = true;

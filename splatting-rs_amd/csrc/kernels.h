@@ -70,6 +70,15 @@ struct AttnArgs {
 };
 void attention(const Exec& ex, const AttnArgs& a);
 
+// Statically allocated device scratch for the key-slice partials of attention launches that
+// may not allocate: ATTN_SCRATCH_BYTES on every GPU the library runs on. attention_scratch()
+// returns its address on `device` (looked up on first use, which must be with that device
+// current); an Exec whose ws points at {that address, ATTN_SCRATCH_BYTES} runs attention()
+// on it.
+constexpr size_t ATTN_SCRATCH_BYTES = size_t(64) << 20;
+constexpr int ATTN_SCRATCH_DEVICES = 64;
+void* attention_scratch(int device);
+
 // LayerNorm over the last dim of rows: out[r] = LN(in[row_in(r)]) * w + b (w/b nullable);
 // row_in(r) = (r / rm_P) * rm_n + rm_off + r % rm_P when rm_P > 0, else r.
 void layer_norm(const Exec& ex, int in_dt, const void* in, long ldin, int out_dt, void* out, long ldout,

@@ -525,6 +525,7 @@ std::vector<float> uv_table(int channels, int rows, int cols, double aspect) {
 
 Context::Context(int dev) : device(dev) {
   SPLAT_HIP(hipSetDevice(dev));
+  attn_scratch = attention_scratch(dev);
   SPLAT_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   SPLAT_HIP(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking));
   SPLAT_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));

@@ -277,6 +277,9 @@ class Context {
   // Both are event records / waits, so a captured forward captures the branch too.
   hipStream_t aux = nullptr;
   Workspace ws2;
+  // This device's statically allocated attention scratch (attention_scratch), looked up at
+  // creation: the allocation-free attention entry point's partials.
+  void* attn_scratch = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   Exec fork(const Exec& on);
   void join(const Exec& on);

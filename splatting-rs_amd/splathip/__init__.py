@@ -104,6 +104,8 @@ SIGNATURES = {
     "splat_kernel_gemm": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int,
                                     C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
     "splat_kernel_attention": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "splat_kernel_attention_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                                 C.c_int]),
     "splat_profile_begin": (C.c_int, [C.c_void_p]),
     "splat_profile_end": (C.c_int, [C.c_void_p, C.POINTER(KernelStatC), C.c_int, C.POINTER(C.c_int)]),
     "splat_kernel_conv2d": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
@@ -351,6 +353,10 @@ class Context:
 
     def kernel_attention(self, dtype: int, qkv: int, out: int, S: int, L: int, heads: int):
         self.check(self._lib.splat_kernel_attention(self.handle, dtype, C.c_void_p(qkv), C.c_void_p(out), S, L, heads))
+
+    def kernel_attention_noalloc(self, dtype: int, qkv: int, out: int, S: int, L: int, heads: int):
+        self.check(self._lib.splat_kernel_attention_noalloc(self.handle, dtype, C.c_void_p(qkv), C.c_void_p(out), S, L,
+                                                            heads))
 
     def kernel_conv2d(self, dtype, inp, V, H, W, Cin, w, Cout, ldw, ks, stride, bias, relu_in, act, res, out):
         self.check(self._lib.splat_kernel_conv2d(self.handle, dtype, C.c_void_p(inp), V, H, W, Cin, C.c_void_p(w), Cout,
