@@ -5,12 +5,17 @@ feed-forward network path performs. Only `tests/`, `__graft_entry__.smoke()` and
 `cpu_baseline` leg of `bench.py` may import this package, and only as the checker or the
 timed CPU baseline: the product (the HIP library) never calls it.
 
-Each function cites the reference file:line it follows. How each one is pinned (known-answer
-tests from the reference's own unit tests, library routines, closed forms, brute force) is
-listed in tests/test_oracle.py; the composite network order is pinned only by this
-restatement (the reference has no network-level golden vector: depthanything3-rs/README.md
-and mapanything-rs/README.md state its numerics are unchecked), so full-forward parity is
-"parity unpinned" beyond the per-function pins.
+Each function cites the reference file:line it follows. How each one is pinned: the
+elementary functions by known-answer tests from the reference's own unit tests, library
+routines, closed forms and brute force (tests/test_oracle.py); the composite functions
+(transformer block, residual units, fusion blocks and chains, both DPT heads, camera, pose and
+scale heads, dense_output, the info-sharing transformer and the MapAnything assembly) by closed
+forms under structured weights that a swapped operand or reordered op fails
+(tests/test_oracle_composites.py). The reference has no network-level golden vector
+(depthanything3-rs/README.md and mapanything-rs/README.md state its numerics are unchecked);
+what only candle itself could pin (its gelu_erf approximation, LayerNorm statistic precision,
+bf16 rounding points between ops, Metal sdpa) stays "parity unpinned" and the tolerances
+absorb it.
 
 Candle op semantics restated here with PyTorch CPU library routines (the un-vendored
 candle-core/candle-nn 0.11.0 ops of the reference, Cargo.lock:668-731):
