@@ -106,28 +106,110 @@ def make_step(ctx, cfg, spec, images_dev, torch):
     return step, outs
 
 
-def cpu_baseline(cfg, spec, weights, seed):
+def host_cpu():
+    """What the host offers this process: nproc, the CPUs it may run on, the CPU model, and
+    the thread count the job is given (OMP_NUM_THREADS: this pool gives a one-GPU job 16)."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, affinity)
+    return {"nproc": nproc, "affinity_cpus": affinity, "job_threads": max(1, min(share, affinity)), "cpu_model": model}
+
+
+def _oracle_forward(cfg, spec, p, images):
+    from oracle import da3 as OD
+    from oracle import mapanything as OM
+    if cfg.model == "da3":
+        OD.forward_raw(p, spec, images)
+    else:
+        OM.forward(p, spec, images, encoder_only=cfg.encoder_only)
+
+
+def cpu_baseline(cfg, spec, weights, seed, threads, host):
     """The CPU oracle (torch fp32, a restatement of the reference, not candle) timed on a
     bounded sample of the workload: the full forward up to 6 views, else the same
     architecture on 6 of the views (the encoder-only config stays encoder-only)."""
     import torch
     from splathip import synth
-    from oracle import da3 as OD
-    from oracle import mapanything as OM
-    threads = max(1, min(16, os.cpu_count() or 1))
     torch.set_num_threads(threads)
     views = min(cfg.views, 6)
     images = synth.config_images(cfg, seed)[:views]
     p = {k: torch.from_numpy(v) for k, v in weights.items()}
     t = time.perf_counter()
-    if cfg.model == "da3":
-        OD.forward_raw(p, spec, images)
-    else:
-        OM.forward(p, spec, images, encoder_only=cfg.encoder_only)
+    _oracle_forward(cfg, spec, p, images)
     dt = time.perf_counter() - t
     return {"value": views / dt, "unit": "views/s", "cores": threads, "kind": "port",
             "sample": f"{views}-view forward of the {cfg.key} architecture at {cfg.height}x{cfg.width}, fp32 "
-                      f"torch-CPU restatement of the reference (not candle), {dt:.1f} s"}
+                      f"torch-CPU restatement of the reference (not candle), {dt:.1f} s on {threads} threads",
+            "nproc": host["nproc"], "affinity_cpus": host["affinity_cpus"], "cpu_model": host["cpu_model"]}
+
+
+def cpu_one_thread_c2(seed):
+    """BASELINE config 2 (DA3-Small, 6 views 378x504) on one thread, fp32 restatement: the
+    counterpart of the reference's own single-thread number (23.5 s for the same network and
+    views on an M5 core, wasm32; instantsplat-rs/web/README.md:35-38)."""
+    import torch
+    from splathip import specs, synth
+    cfg = specs.CONFIGS["C2"]
+    spec = specs.DA3_VARIANTS[cfg.spec]
+    w = synth.generate(synth.da3_shapes(spec), seed=seed)
+    p = {k: torch.from_numpy(v) for k, v in w.items()}
+    images = synth.config_images(cfg, seed + 1)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        t = time.perf_counter()
+        _oracle_forward(cfg, spec, p, images)
+        dt = time.perf_counter() - t
+    finally:
+        torch.set_num_threads(prev)
+    return {"seconds": dt, "views_per_s": cfg.views / dt, "threads": 1, "kind": "port",
+            "sample": "C2: DA3-Small, 6 views 378x504, full forward, fp32 torch-CPU restatement (not candle)"}
+
+
+def time_config(ctx, key, seed, steps, warmup, tmp, torch):
+    """GPU ms/forward of another configuration (graph replay, inputs resident in HBM), for the
+    extra keys of the line."""
+    import splathip
+    from splathip import specs, synth
+    cfg = specs.CONFIGS[key]
+    spec, _ = build_model(ctx, cfg, seed, tmp)
+    images = torch.from_numpy(synth.config_images(cfg, seed + 1)).cuda()
+    step, _ = make_step(ctx, cfg, spec, images, torch)
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    torch.cuda.synchronize()
+    for _ in range(max(1, warmup)):
+        step()
+    ctx.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    ctx.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    log(f"{key}: {ms:.3f} ms/forward (events)")
+    return {"ms_per_forward": ms, "views_per_s": cfg.views / (ms * 1e-3), "dtype": cfg.dtype,
+            "workload": f"{key}: {cfg.description}"}
+
+
+def time_host_io(ctx, cfg, seed, reps):
+    """ms per forward through the host-pointer entry point (images copied in, outputs copied
+    out over PCIe, synchronous), the reference's calling convention."""
+    from splathip import synth
+    images = synth.config_images(cfg, seed + 1)
+    fwd = (lambda: ctx.da3_forward_raw(images)) if cfg.model == "da3" else \
+          (lambda: ctx.ma_encode(images)) if cfg.encoder_only else (lambda: ctx.ma_forward(images))
+    fwd()
+    t = time.perf_counter()
+    for _ in range(reps):
+        fwd()
+    return 1e3 * (time.perf_counter() - t) / reps
 
 
 def main():
@@ -139,6 +221,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graphs", action="store_true", help="eager launches instead of HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the extra keys (other configurations' GPU times, host-I/O time, 1-thread C2 CPU time)")
     ap.add_argument("--profile-out", default="", help="write the per-kernel-class profile as JSON here")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB -> 256 MiB streaming kernel (torch.neg on fp32), the "
@@ -164,6 +248,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     cfg = specs.CONFIGS[args.config]
+    host = host_cpu()
     ctx = splathip.Context(0)
     with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
         spec, weights = build_model(ctx, cfg, args.seed, tmp)
@@ -216,11 +301,26 @@ def main():
     mfma_flops = sum(s["flops"] for s in stats if s["name"] in MFMA_KERNELS)
     mfma_ms = sum(s["ms"] for s in stats if s["name"] in MFMA_KERNELS)
 
+    extra = {}
+    if not args.no_extra:
+        extra["host_io_ms_per_forward"] = time_host_io(ctx, cfg, args.seed, max(3, args.steps // 4))
+        log(f"{cfg.key} through host buffers (PCIe in and out): {extra['host_io_ms_per_forward']:.3f} ms/forward")
+        others = {}
+        with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+            for key in ("C1", "C2"):
+                if key != cfg.key:
+                    others[key] = time_config(ctx, key, args.seed, args.steps, args.warmup, tmp, torch)
+        extra["other_configs"] = others
+
     cpu = None
     if not args.no_cpu_baseline:
-        log("timing the CPU baseline ...")
-        cpu = cpu_baseline(cfg, spec, weights, args.seed + 1)
+        log(f"timing the CPU baseline ({host['job_threads']} threads of {host['nproc']}, {host['cpu_model']}) ...")
+        cpu = cpu_baseline(cfg, spec, weights, args.seed + 1, host["job_threads"], host)
         log(f"cpu baseline: {cpu}")
+        if not args.no_extra:
+            log("timing C2 on one CPU thread ...")
+            extra["cpu_c2_one_thread"] = cpu_one_thread_c2(args.seed)
+            log(f"cpu C2 one thread: {extra['cpu_c2_one_thread']}")
 
     V = cfg.views
     R, Cc = cfg.height // 14, cfg.width // 14
@@ -249,6 +349,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
     }
+    line.update(extra)
     print(json.dumps(line), flush=True)
     ctx.close()
 
