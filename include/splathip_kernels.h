@@ -18,6 +18,27 @@ extern "C" {
 int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, const void* W, int N, int ldw,
                       const float* bias, int act, void* C, int out_f32);
 
+/* The pre-norm block's GEMMs with its LayerNorm folded in (depthanything3-rs/src/vit_block.rs:151,165;
+ * mapanything-rs/src/vit_block.rs:99,105: norm1 -> qkv, norm2 -> fc1), as the forwards run them.
+ * Row statistics: (sum, sum of squares) of each row per group of `group` (64 or 128) columns.
+ *  ln_in != NULL (consumer): A [M, K] holds the rows before the norm, ln_in [M, K/group, 2] their
+ *    statistics; W and c1 the folded weights (W = gamma (.) W_lin along K, c1[n] = sum_k W[n, k])
+ *    and bias = b_lin + W_lin beta; out = act(rstd * (acc - mean * c1[n]) + bias[n]) with each
+ *    row's mean and rstd over K (biased variance, eps inside the root); K/group <= 16.
+ *  res != NULL (producer, the residual epilogue of proj / fc2): out = res + gamma[n] * (acc +
+ *    bias[n]), res and out fp32 [M, N]; with ln_out != NULL also the statistics of the output
+ *    rows [M, N/group, 2] and, with copy != NULL, the rows in `dtype` [M, N] (the consumer's A).
+ *  Otherwise as splat_kernel_gemm. */
+int splat_kernel_gemm_ln(splat_ctx* ctx, int dtype, const void* A, int M, int K, const void* W, int N, int ldw,
+                         const float* bias, int act, const float* ln_in, const float* c1, float eps,
+                         const float* gamma, const float* res, float* ln_out, void* copy, int group, void* out,
+                         int out_f32);
+
+/* Row statistics of fp32 rows x [rows, n] (n a multiple of group, 64 or 128) in the layout above,
+ * and the rows converted to `dtype` into copy [rows, n] when copy != NULL. */
+int splat_kernel_ln_stats(splat_ctx* ctx, const float* x, int rows, int n, int group, float* stats, int dtype,
+                          void* copy);
+
 /* out[s*L + t, h*64 + e] = softmax(q k^T / 8) v for every sequence s < S and head h < heads,
  * reading q, k and v from a [S*L, 3*heads*64] qkv matrix (q | k | v column blocks). */
 int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads);

@@ -373,6 +373,59 @@ int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, co
   });
 }
 
+int splat_kernel_gemm_ln(splat_ctx* ctx, int dtype, const void* A, int M, int K, const void* W, int N, int ldw,
+                         const float* bias, int act, const float* ln_in, const float* c1, float eps,
+                         const float* gamma, const float* res, float* ln_out, void* copy, int group, void* out,
+                         int out_f32) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
+    SPLAT_CHECK(act >= 0 && act <= 2, BAD_ARGUMENT, "act");
+    SPLAT_CHECK(group == 64 || group == 128, BAD_ARGUMENT, "statistics group: 64 or 128 columns");
+    SPLAT_CHECK(!ln_in || K % group == 0, BAD_ARGUMENT, "folded LayerNorm: K must be a multiple of the group");
+    SPLAT_CHECK(!(ln_in && res), BAD_ARGUMENT, "a folded LayerNorm has no residual epilogue");
+    SPLAT_CHECK(!res || out_f32, BAD_ARGUMENT, "residual epilogue: fp32 output");
+    SPLAT_CHECK(!ln_out || res, BAD_ARGUMENT, "row statistics come from the residual epilogue");
+    GemmArgs g;
+    g.dt = dtype == SPLAT_F32 ? F32 : BF16;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.A = A;
+    g.lda = K;
+    g.W = W;
+    g.ldw = ldw;
+    g.bias = bias;
+    g.act = act;
+    g.out = out;
+    g.ldc = N;
+    g.out_f32 = out_f32;
+    if (ln_in) {
+      g.ln_in = ln_in;
+      g.ln_parts = K / group;
+      g.ln_c1 = c1;
+      g.ln_eps = eps;
+    }
+    if (res) {
+      g.gamma = gamma;
+      g.res = res;
+      g.ldres = N;
+      g.res_f32 = 1;
+      g.ln_out = ln_out;
+      g.ln_group = group;
+      g.ln_copy = ln_out ? copy : nullptr;
+    }
+    gemm_now(C(ctx), g);
+  });
+}
+
+int splat_kernel_ln_stats(splat_ctx* ctx, const float* x, int rows, int n, int group, float* stats, int dtype,
+                          void* copy) {
+  return guard(C(ctx), [&] {
+    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
+    ln_stats(C(ctx)->ex, x, n, rows, n, group, stats, dtype == SPLAT_F32 ? F32 : BF16, copy);
+  });
+}
+
 int splat_kernel_attention_noalloc(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads) {
   return guard(C(ctx), [&] {
     Context* c = C(ctx);

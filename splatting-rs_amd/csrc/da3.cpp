@@ -169,7 +169,10 @@ void Da3Model::forward(const float* images, int V, int H, int W, const splat_da3
       const int strat = (V >= 3 && spec_.alt_start >= 1) ? strategy_ : 0;
       select_reference_view(ex, cur, V, n, d, strat, ref);
     }
-    if (i == spec_.alt_start) set_camera_tokens(ex, cur, V, n, d, camera_, ref);
+    if (i == spec_.alt_start) {
+      set_camera_tokens(ex, cur, V, n, d, camera_, ref);
+      if (s.ln_src == cur) block_ln_refresh(ctx_, dt_, cur, V, d, s, 1, n, 0);  // the rewritten class rows
+    }
     const bool across = i >= spec_.alt_start && i % 2 == 1;
     const int rope = i >= spec_.alt_start ? (across ? 2 : 1) : 0;
     float* dst = cur == within ? (cur == X0 ? X1 : X0) : cur;

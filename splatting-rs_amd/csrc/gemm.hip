@@ -20,6 +20,7 @@ namespace splat {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16> {
@@ -100,11 +101,11 @@ __device__ inline void load8(const void* p, long i, bool f32, float* v) {
   }
 }
 
-// Store of 8 consecutive output values (16-byte aligned, all inside the output).
+// Store of 8 consecutive values (16-byte aligned, all inside the array) as fp32 or as T.
 template <typename T>
-__device__ inline void store8(const GemmArgs& p, const float* v, long idx) {
-  if (p.out_f32 || sizeof(T) == 4) {
-    float* o = reinterpret_cast<float*>(p.out) + idx;
+__device__ inline void store8_to(void* base, bool f32, const float* v, long idx) {
+  if (f32 || sizeof(T) == 4) {
+    float* o = reinterpret_cast<float*>(base) + idx;
     *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
     *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
   } else {
@@ -113,12 +114,18 @@ __device__ inline void store8(const GemmArgs& p, const float* v, long idx) {
     u.y = pack_bf16x2(v[2], v[3]);
     u.z = pack_bf16x2(v[4], v[5]);
     u.w = pack_bf16x2(v[6], v[7]);
-    *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p.out) + idx) = u;
+    *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(base) + idx) = u;
   }
+}
+// Store of 8 consecutive output values.
+template <typename T>
+__device__ inline void store8(const GemmArgs& p, const float* v, long idx) {
+  store8_to<T>(p.out, p.out_f32, v, idx);
 }
 
 // Epilogue of 8 consecutive columns n..n+7 of row m: bias, activation, table add, LayerScale,
-// residuals, post-residual activation, store. `vec`: all of them exist and every operand is 16-byte aligned for them.
+// residuals, post-residual activation, store. `vec`: all of them exist and every operand is
+// 16-byte aligned for them.
 template <typename T>
 __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool vec) {
   const long row = p.rm_P ? (m / p.rm_P) * p.rm_n + p.rm_off + m % p.rm_P : m;
@@ -171,9 +178,27 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
 // block must be past its last read of the main-loop LDS.
 // EPI_PART: split-K slice, the raw fp32 sums go to the partial buffer; a reduce kernel adds
 // the slices and applies the full epilogue.
-enum EpiKind { EPI_BIAS = 0, EPI_RES = 1, EPI_FULL = 2, EPI_PART = 3, EPI_HEAD = 4 };
+// EPI_LN: EPI_BIAS with the folded LayerNorm of the A rows (GemmArgs::ln_in): rstd * (acc -
+// mean * c1), with (rstd, -rstd * mean) of each tile row reduced from its partial statistics by
+// one thread at the kernel's start (the loads go out ahead of the first operand tiles) and kept
+// in LDS for the epilogue. EPI_RESLN: EPI_RES that also emits the statistics of its output rows
+// (GemmArgs::ln_out) and their copy in the GEMM's dtype: each 4-lane group of a row sums its 32
+// columns (DPP), the sums meet in LDS past the slabs, and after the last slab the block writes
+// one (sum, sum of squares) pair per row and column group.
+enum EpiKind { EPI_BIAS = 0, EPI_RES = 1, EPI_FULL = 2, EPI_PART = 3, EPI_HEAD = 4, EPI_LN = 5, EPI_RESLN = 6 };
+
+// Sum over the G consecutive lanes of a group (G = 4, 8 or 16, groups aligned), left in every
+// lane of the group: quad swaps, then the half-row and row mirrors.
+template <int G> __device__ __forceinline__ float group_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, true));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, true));
+  if (G >= 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, true));
+  if (G >= 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, true));
+  return v;
+}
 
 constexpr int slab_ld(int tn) { return tn * 32 + 4; }  // +4 floats: conflict-free 16-byte row reads
+
 
 template <int TM, int TN>
 __device__ __forceinline__ void stage_slab(const f32x16 (&acc)[TM][TN], int i, float* slab, int lane) {
@@ -200,9 +225,12 @@ __device__ __forceinline__ void read8(const float* q, float* v) {
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// `lnab` (EPI_LN): (rstd, -rstd * mean) of this wave's rows in LDS. `lnp` (EPI_RESLN): this
+// wave's corner of the LDS array of 32-column sums, lnp_ld a row.
 template <typename T, int TM, int TN, int EPI>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long wrow0, long wcol0, float* slab,
-                                         int lane, bool vec, float* part = nullptr) {
+                                         int lane, bool vec, float* part = nullptr, const float* lnab = nullptr,
+                                         float* lnp = nullptr, int lnp_ld = 0) {
   constexpr int COLS = TN * 32, LD = slab_ld(TN), RUNS = COLS / 8;
   if constexpr (EPI == EPI_PART) {
     // rows of 8 columns: n < N implies n + 8 <= ldp (ldp is N rounded up to 8)
@@ -236,20 +264,31 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
       slab_done();
     }
   } else {
+    constexpr bool RES = EPI == EPI_RES || EPI == EPI_RESLN;
     constexpr int IT = 32 * RUNS / 64;   // runs per lane per slab
     constexpr int CH = IT < 4 ? IT : 4;  // runs whose residual loads are in flight together
     static_assert(64 % RUNS == 0 && IT % CH == 0, "run layout");
     const int cc = (lane % RUNS) * 8, rsub = lane / RUNS;
     const long n = wcol0 + cc;
     const bool nok = n < p.N;  // the host guarantees that a run starting inside the output lies in it
-    float cb[8], cg[8];
+    float cb[8], cg[8], c1[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) { cb[k] = 0.f; cg[k] = 1.f; }
+    for (int k = 0; k < 8; ++k) { cb[k] = 0.f; cg[k] = 1.f; c1[k] = 0.f; }
     if (nok && p.bias) load8(p.bias, n, true, cb);
-    if (EPI == EPI_RES && nok && p.gamma) load8(p.gamma, n, true, cg);
+    if (RES && nok && p.gamma) load8(p.gamma, n, true, cg);
+    if (EPI == EPI_LN && nok) load8(p.ln_c1, n, true, c1);
     const bool rf = p.res_f32 || sizeof(T) == 4, rf2 = p.res2_f32 || sizeof(T) == 4;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+      float la[IT], lb[IT];  // folded LayerNorm of this lane's rows
+      if constexpr (EPI == EPI_LN) {
+#pragma unroll
+        for (int t = 0; t < IT; ++t) {
+          const float2 ab = *reinterpret_cast<const float2*>(lnab + (i * 32 + rsub + t * (64 / RUNS)) * 2);
+          la[t] = ab.x;
+          lb[t] = ab.y;
+        }
+      }
       stage_slab<TM, TN>(acc, i, slab, lane);
 #pragma unroll
       for (int t0 = 0; t0 < IT; t0 += CH) {
@@ -259,9 +298,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
           const int rr = rsub + (t0 + t) * (64 / RUNS);
           const long m = wrow0 + i * 32 + rr;
           read8(slab + rr * LD + cc, v[t]);
-          if (EPI == EPI_RES && p.res && nok && m < p.M) load8(p.res, m * p.ldres + n, rf, rv[t]);
+          if (RES && p.res && nok && m < p.M) load8(p.res, m * p.ldres + n, rf, rv[t]);
         }
-        if (EPI == EPI_RES && p.res2) {  // second residual (the DPT residual units' skip input)
+        if (RES && p.res2) {  // second residual (the DPT residual units' skip input)
 #pragma unroll
           for (int t = 0; t < CH; ++t) {
             const long m = wrow0 + i * 32 + rsub + (t0 + t) * (64 / RUNS);
@@ -275,10 +314,16 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
         }
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
-          const long m = wrow0 + i * 32 + rsub + (t0 + t) * (64 / RUNS);
+          const int rr = rsub + (t0 + t) * (64 / RUNS);
+          const long m = wrow0 + i * 32 + rr;
           float* x = v[t];
+          if constexpr (EPI == EPI_LN) {
 #pragma unroll
-          for (int k = 0; k < 8; ++k) x[k] += cb[k];
+            for (int k = 0; k < 8; ++k) x[k] = fmaf(la[t0 + t], x[k], fmaf(lb[t0 + t], c1[k], cb[k]));
+          } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] += cb[k];
+          }
           if (p.act == ACT_RELU) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) x[k] = fmaxf(x[k], 0.f);
@@ -286,7 +331,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
 #pragma unroll
             for (int k = 0; k < 8; ++k) x[k] = gelu_erf(x[k]);
           }
-          if (EPI == EPI_RES) {
+          if (RES) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) x[k] *= cg[k];
             if (p.res) {
@@ -294,7 +339,26 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
               for (int k = 0; k < 8; ++k) x[k] += rv[t][k];
             }
           }
-          if (nok && m < p.M) store8<T>(p, x, m * p.ldc + n);
+          const bool ok = nok && m < p.M;
+          if constexpr (EPI == EPI_RESLN) {
+            float s = 0.f, q = 0.f;
+            if (ok) {
+#pragma unroll
+              for (int k = 0; k < 8; ++k) {
+                s += x[k];
+                q = fmaf(x[k], x[k], q);
+              }
+            }
+            s = group_sum<4>(s);  // the 4 lanes of one 32-column group
+            q = group_sum<4>(q);
+            if ((lane & 3) == 0) {
+              float* dst = lnp + ((i * 32 + rr) * lnp_ld + cc / 32) * 2;
+              dst[0] = s;
+              dst[1] = q;
+            }
+            if (ok && p.ln_copy) store8_to<T>(p.ln_copy, false, x, m * p.ldc + n);  // the GEMM's dtype
+          }
+          if (ok) store8<T>(p, x, m * p.ldc + n);
         }
       }
       slab_done();
@@ -386,7 +450,9 @@ __device__ __forceinline__ void head_epilogue(const GemmArgs& p, f32x16 (&acc)[T
 inline int epi_kind(const GemmArgs& a) {
   if (a.hw3) return EPI_HEAD;
   if (!a.epi_vec || a.rm_P || a.store != STORE_ROWS || a.addtab || a.act_post || (a.res2 && !a.res)) return EPI_FULL;
-  return (a.res || a.gamma) ? EPI_RES : EPI_BIAS;
+  if (a.ln_in) return (a.res || a.gamma || a.res2) ? EPI_FULL : EPI_LN;  // EPI_FULL: refused by gemm()
+  if (a.res || a.gamma) return (a.ln_out && !a.res2) ? EPI_RESLN : EPI_RES;
+  return EPI_BIAS;
 }
 
 // Whether the 8-column vector path is valid for every run of a launch (host side).
@@ -394,11 +460,13 @@ inline bool epi_vec_ok(const GemmArgs& a, size_t es) {
   auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   const size_t oes = a.out_f32 ? 4 : es;
   bool ok = a.N % 8 == 0 && al(a.out) && (a.bias == nullptr || al(a.bias)) && (a.gamma == nullptr || al(a.gamma)) &&
-            (a.addtab == nullptr || al(a.addtab));
+            (a.addtab == nullptr || al(a.addtab)) && (a.ln_c1 == nullptr || al(a.ln_c1)) &&
+            (a.ln_copy == nullptr || al(a.ln_copy));
   if (a.store == STORE_CONVT) ok = ok && a.ct_Cout % 8 == 0;
   else ok = ok && (a.ldc * oes) % 16 == 0;
   if (a.res) ok = ok && al(a.res) && (a.ldres * (a.res_f32 ? 4 : es)) % 16 == 0;
   if (a.res2) ok = ok && al(a.res2) && (a.ldres2 * (a.res2_f32 ? 4 : es)) % 16 == 0;
+  if (a.ln_copy) ok = ok && (a.ldc * es) % 16 == 0;
   return ok;
 }
 
@@ -593,7 +661,11 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   constexpr int STAGE = (BM + BN) * RB;
   static_assert((STAGES - 1) * LPT <= 63, "vmcnt range");
   static_assert(STAGES * STAGE >= NW * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the ring");
+  static_assert(EPI != EPI_LN || NW * 64 >= BM, "folded LayerNorm: a thread per tile row");
+  static_assert(EPI != EPI_RESLN || STAGES * STAGE >= (NW * 32 * slab_ld(TN) + BM * (BN / 32) * 2) * 4,
+                "row statistics: the 32-column sums past the epilogue slabs");
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+  __shared__ __attribute__((aligned(16))) float lnab[EPI == EPI_LN ? 2 * BM : 2];  // (rstd, -rstd * mean) a row
 
   // the wave index is uniform: every LDS destination of the DMA loads is scalar arithmetic
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -738,11 +810,36 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   // the barrier, and the loads of tile kt + 2 go into the barrier step.
   constexpr bool SPREAD = STAGES >= 3;
   constexpr int AHEAD = SPREAD ? STAGES - 1 : STAGES;  // tile kt loads tile kt + AHEAD
+  // Folded LayerNorm: thread r < BM loads the partial statistics of tile row r ahead of the
+  // operand tiles (up to 16 pairs) and reduces them once those tiles are resident.
+  float2 lnv[EPI == EPI_LN ? 16 : 1];
+  const long lnm = m0 + tid;
+  if constexpr (EPI == EPI_LN) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      lnv[j] = (tid < BM && lnm < p.M && j < p.ln_parts)
+                   ? *reinterpret_cast<const float2*>(p.ln_in + (lnm * p.ln_parts + j) * 2)
+                   : make_float2(0.f, 0.f);
+  }
 #pragma unroll
   for (int s = 0; s < AHEAD; ++s)
 #pragma unroll
     for (int l = 0; l < LPT; ++l) issue_one(s, s, l, std::false_type{});
   wait_vmcnt<(AHEAD - 1) * LPT>();
+  if constexpr (EPI == EPI_LN) {
+    if (tid < BM) {
+      float s = 0.f, q = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        s += lnv[j].x;
+        q += lnv[j].y;
+      }
+      const float inv = 1.f / float(p.K), mean = s * inv;
+      const float rstd = rsqrtf(fmaxf(q * inv - mean * mean, 0.f) + p.ln_eps);
+      lnab[2 * tid] = rstd;
+      lnab[2 * tid + 1] = -rstd * mean;
+    }
+  }
   __syncthreads();
   // Fragments of the next k-step (of this tile, or step 0 of the next tile) are read while the
   // matrix cores work on the current one.
@@ -840,8 +937,29 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
     head_epilogue<T, BM, BN, WM, WN, TM, TN>(p, acc, m0, wm, wn, reinterpret_cast<float*>(smem), wave, lane, tid);
   } else {
     float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
+    constexpr int LNLD = BN / 32;  // 32-column sums per tile row (EPI_RESLN)
+    float* lnp = reinterpret_cast<float*>(smem) + NW * 32 * slab_ld(TN);
     epilogue<T, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
-                                EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr);
+                             EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr, lnab + wm * (BM / WM) * 2,
+                             lnp + (wm * (BM / WM) * LNLD + wn * (BN / WN) / 32) * 2, LNLD);
+    if constexpr (EPI == EPI_RESLN) {
+      // every wave's 32-column sums are in LDS: one (sum, sum of squares) per row and group
+      __syncthreads();
+      const int gw = p.ln_group / 32, ng = BN / p.ln_group, parts = p.N / p.ln_group;
+      for (int idx = tid; idx < BM * ng; idx += NW * 64) {
+        const int r = idx / ng, gg = idx - r * ng;
+        const long m = m0 + r, nc = n0 + gg * p.ln_group;
+        if (m < p.M && nc < p.N) {
+          const float* a = lnp + (r * LNLD + gg * gw) * 2;
+          float s = 0.f, q = 0.f;
+          for (int c = 0; c < gw; ++c) {
+            s += a[2 * c];
+            q += a[2 * c + 1];
+          }
+          *reinterpret_cast<float2*>(p.ln_out + (m * parts + nc / p.ln_group) * 2) = make_float2(s, q);
+        }
+      }
+    }
   }
 }
 
@@ -869,12 +987,16 @@ constexpr int GEMM_CUS = 256;  // MI355X compute units: one "round" of resident 
 
 // TAP_ONLY: an instantiation that serves per-tap convolutions only (the 32-element k-tiles for
 // maps whose Cin is a multiple of 32 but not of 64).
+// Returns whether the launch wrote the row statistics (and copy) a producer (ln_out) asks for.
 template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 128 / sizeof(T), int MINB = 1,
           bool TAP_ONLY = false>
-static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
+static bool launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   static_assert(MINB == 1 || MINB * STAGES * (BM + BN) * BK * sizeof(T) <= 160 * 1024, "LDS of MINB blocks per CU");
   const int tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
-  const int epi = S > 1 ? EPI_PART : epi_kind(a);
+  int epi = S > 1 ? EPI_PART : epi_kind(a);
+  if (epi == EPI_RESLN && (a.amode != A_ROWS || TAP_ONLY || BN % a.ln_group != 0)) epi = EPI_RES;  // statistics afterwards
+  SPLAT_CHECK(!a.ln_in || (epi == EPI_LN && a.amode == A_ROWS && !TAP_ONLY), BAD_ARGUMENT,
+              "gemm: a folded LayerNorm needs plain rows, a vectorisable epilogue and no split-K");
   GemmArgs b = a;
   if (S > 1) {
     b.part = static_cast<float*>(ex.ws->ptr);
@@ -900,6 +1022,8 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
       if (epi == EPI_PART) SPLAT_GO(A_ROWS, false, EPI_PART);
       else if (epi == EPI_BIAS) SPLAT_GO(A_ROWS, false, EPI_BIAS);
       else if (epi == EPI_RES) SPLAT_GO(A_ROWS, false, EPI_RES);
+      else if (epi == EPI_LN) SPLAT_GO(A_ROWS, false, EPI_LN);
+      else if (epi == EPI_RESLN) SPLAT_GO(A_ROWS, false, EPI_RESLN);
       else SPLAT_GO(A_ROWS, false, EPI_FULL);
     }
   } else if (tap) {
@@ -929,6 +1053,7 @@ static void launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
     hipLaunchKernelGGL(splitk_reduce_kernel<T>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b, S);
     SPLAT_HIP(hipGetLastError());
   }
+  return epi == EPI_RESLN;
 }
 
 // Tile configurations of the bf16 path: block tile, and how many blocks share a CU.
@@ -993,7 +1118,7 @@ static BfCfg pick_bf16(const GemmArgs& a) {
 // one round. The slices write fp32 partials; a second kernel sums them and applies the
 // epilogue (the DPT head's coarse-level convs: M = 1596, K = 6912, 14 tiles of 256x128).
 static int split_factor(const GemmArgs& a, BfCfg c) {
-  if (a.hw3) return 1;  // the fused head needs whole tiles
+  if (a.hw3 || a.ln_in) return 1;  // the fused head needs whole tiles, a folded LayerNorm whole rows of K
   const BfShape sh = bf_shape(c);
   const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
   const long slots = long(GEMM_CUS) * sh.per_cu;
@@ -1026,7 +1151,7 @@ static BfCfg pick_f32(const GemmArgs& a) {
   return pick;
 }
 
-static void launch_f32_auto(const Exec& ex, const GemmArgs& a) {
+static bool launch_f32_auto(const Exec& ex, const GemmArgs& a) {
   const BfCfg c = pick_f32(a);
   int S = split_factor(a, c);
   if (S > 1 && !(ex.ws && ex.ws->ptr && ex.ws->cap >= split_bytes(a, S))) S = 1;
@@ -1039,7 +1164,7 @@ static void launch_f32_auto(const Exec& ex, const GemmArgs& a) {
   }
 }
 
-static void launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
+static bool launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
   const BfCfg c = pick_bf16(a);
   int S = split_factor(a, c);
   if (S > 1 && !(ex.ws && ex.ws->ptr && ex.ws->cap >= split_bytes(a, S))) S = 1;
@@ -1086,14 +1211,16 @@ static bool mfma_path_ok(const GemmArgs& a) {
 }
 
 template <typename T>
-static void launch_typed(const Exec& ex, const GemmArgs& a) {
+static bool launch_typed(const Exec& ex, const GemmArgs& a) {
   if (mfma_path_ok(a)) return sizeof(T) == 2 ? launch_bf16_auto(ex, a) : launch_f32_auto(ex, a);
-  SPLAT_CHECK(a.hw3 == nullptr, BAD_ARGUMENT, "gemm: the fused head needs the MFMA path");
+  SPLAT_CHECK(a.hw3 == nullptr && a.ln_in == nullptr, BAD_ARGUMENT,
+              "gemm: the fused head and the folded LayerNorm need the MFMA path");
   const long tiles128 = (long)cdiv(a.M, 128) * cdiv(a.N, 128);
   if (a.N <= 32) launch_cfg<T, 256, 32, 4, 1>(ex, a);
   else if (a.N <= 64) launch_cfg<T, 256, 64, 4, 1>(ex, a);
   else if (tiles128 >= 512) launch_cfg<T, 128, 128, 2, 2>(ex, a);
   else launch_cfg<T, 64, 128, 1, 4>(ex, a);
+  return false;
 }
 
 void gemm(const Exec& ex, const GemmArgs& args) {
@@ -1113,6 +1240,16 @@ void gemm(const Exec& ex, const GemmArgs& args) {
   if (a.store == STORE_CONVT)
     SPLAT_CHECK((long)a.ct_s * a.ct_s * a.ct_Cout == a.N && (long)a.V * a.ct_R * a.ct_C == a.M, BAD_ARGUMENT,
                 "gemm: convT geometry");
+  if (a.ln_in)
+    SPLAT_CHECK(a.ln_c1 && a.ln_eps > 0.f && a.ln_parts > 0 && a.ln_parts <= 16 && a.amode == A_ROWS && !a.res &&
+                    !a.gamma && !a.res2 && !a.addtab && !a.rm_P && !a.act_post && a.store == STORE_ROWS && a.epi_vec,
+                BAD_ARGUMENT, "gemm: a folded LayerNorm needs plain aligned rows, a bias/activation epilogue and "
+                              "at most 16 partials a row");
+  if (a.ln_out)
+    SPLAT_CHECK((a.ln_group == 64 || a.ln_group == 128) && a.N % a.ln_group == 0 && a.out_f32 &&
+                    a.store == STORE_ROWS && !a.rm_P && a.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.ln_copy) & 15) == 0,
+                BAD_ARGUMENT, "gemm: row statistics need fp32 rows and N a multiple of the group");
   if (ex.dry && ex.ws && a.M > 0 && mfma_path_ok(a))  // size the split-K partials of the real run
     ex.ws->need = std::max(ex.ws->need, split_bytes(a, split_factor(a, a.dt == F32 ? pick_f32(a) : pick_bf16(a))));
   if (ex.dry || a.M == 0) return;
@@ -1120,9 +1257,13 @@ void gemm(const Exec& ex, const GemmArgs& args) {
   const double abytes = a.amode == A_ROWS ? double(a.M) * a.K * es : double(a.V) * a.Hi * a.Wi * a.Cin * es;
   const double bytes = abytes + double(a.N) * a.K * es + mn * (a.out_f32 ? 4 : es) +
                        (a.res ? mn * (a.res_f32 ? 4 : es) : 0) + (a.res2 ? mn * (a.res2_f32 ? 4 : es) : 0);
-  ProfScope ps(ex, a.amode == A_ROWS ? "gemm" : "conv_igemm", 2.0 * mn * a.K, bytes);
-  if (a.dt == F32) launch_typed<float>(ex, a);
-  else launch_typed<bf16>(ex, a);
+  bool stats;
+  {
+    ProfScope ps(ex, a.amode == A_ROWS ? "gemm" : "conv_igemm", 2.0 * mn * a.K, bytes);
+    stats = a.dt == F32 ? launch_typed<float>(ex, a) : launch_typed<bf16>(ex, a);
+  }
+  if (a.ln_out && !stats)  // this path's epilogue does not emit them
+    ln_stats(ex, static_cast<const float*>(a.out), a.ldc, a.M, a.N, a.ln_group, a.ln_out, a.dt, a.ln_copy);
 }
 
 }  // namespace splat

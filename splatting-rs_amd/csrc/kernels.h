@@ -19,7 +19,7 @@ enum StoreMode { STORE_ROWS = 0, STORE_CONVT = 1 };
 // A (dtype `dt`): A_ROWS -> row-major [M, lda]; A_CONV -> implicit im2col of an NHWC map
 // [V, Hi, Wi, Cin] for a ks x ks convolution (stride, pad), k = (ky*ks + kx)*Cin + ci.
 // W (dtype `dt`): [N, ldw] row-major; columns K..ldw-1 must be zero and ldw a multiple of 64.
-// Epilogue, in this order: + bias[n]; activation; + addtab[(m % period) * N + n];
+// Epilogue, in this order: folded LayerNorm (ln_in, below); + bias[n]; activation; + addtab[(m % period) * N + n];
 // * gamma[n]; + res[row, n]; + res2[row, n]; store (`out_f32` selects fp32 or `dt`).
 // With rm_P > 0 the stored row is (m / rm_P) * rm_n + rm_off + m % rm_P (also for res/res2).
 // STORE_CONVT scatters a kernel=stride transposed convolution: m = (v, r, c) of an R x C
@@ -52,8 +52,30 @@ struct GemmArgs {
   // [pix, 3] (scaled by *hscale), ho2 confidence, ho3 unambiguous mask (each may be null).
   const float* hw3 = nullptr; const float* hb3 = nullptr; const float* hscale = nullptr; int hhw = 0;
   float* ho0 = nullptr; float* ho1 = nullptr; float* ho2 = nullptr; uint8_t* ho3 = nullptr;
+  // Pre-norm LayerNorm folded into the GEMMs on either side of it (a block's LN -> linear).
+  // Producer (ln_out != null; N a multiple of ln_group, 64 or 128): also writes the statistics
+  //   of its final output rows, ln_out[(m * (N / ln_group) + g) * 2 + {0, 1}] = (sum, sum of
+  //   squares) of row m over columns [g * ln_group, (g + 1) * ln_group), and when ln_copy !=
+  //   null the output rows in the GEMM's dtype, [M, ldc] (the consumer's A operand in bf16).
+  // Consumer (ln_in != null): A holds the rows x before the norm (K columns); row m's mean and
+  //   rstd come from its ln_parts (<= 16) partials in ln_in (biased variance over K, eps
+  //   ln_eps) and the epilogue starts from rstd * (acc - mean * ln_c1[n]) + bias[n].
+  //   W = gamma (.) W_linear (scaled along K), ln_c1[n] = sum_k W[n, k], bias = b_linear +
+  //   W_linear beta, folded at load: linear(LN(x)) up to rounding. Needs plain rows (no
+  //   residual, remap or table) and runs without split-K.
+  float* ln_out = nullptr; int ln_group = 64; void* ln_copy = nullptr;
+  const float* ln_in = nullptr; int ln_parts = 0; const float* ln_c1 = nullptr; float ln_eps = 0.f;
 };
+// A producer whose tile path cannot emit the statistics (split-K, unaligned, tiles narrower
+// than the group) gets them (and the copy) from ln_stats() on its output.
 void gemm(const Exec& ex, const GemmArgs& a);
+
+// Row statistics of fp32 rows in the layout of GemmArgs::ln_out ((sum, sum of squares) per
+// group of `group` columns, 64 or 128; n a multiple of it) and, when copy != null, the rows
+// converted to copy_dt (same row stride). Row r of the launch is row (r / rm_P) * rm_n +
+// rm_off + r % rm_P (rm_P > 0) or r, for the input, the statistics and the copy alike.
+void ln_stats(const Exec& ex, const float* x, long ldx, int rows, int n, int group, float* stats, int copy_dt,
+              void* copy, int rm_P = 0, int rm_n = 0, int rm_off = 0);
 
 // Flash attention, head dim 64, no mask: O = softmax(Q K^T / 8) V per (sequence, head).
 // Row t of sequence s is row s*seq_stride + t of q/k/v (row stride ld elements, head h at

@@ -160,6 +160,55 @@ void layer_norm(const Exec& ex, int in_dt, const void* in, long ldin, int out_dt
 }
 
 // ---------------------------------------------------------------------------------------
+// Row statistics for a LayerNorm folded into the next GEMM (GemmArgs::ln_in): one wave per
+// row, 4 columns a lane; the 16 lanes of a DPP row cover 64 columns, so each 64-column sum is a
+// 16-lane reduction (a 128-column group adds two of them); optional copy of the row in the
+// GEMM's dtype.
+template <typename TO>
+__global__ void __launch_bounds__(256) ln_stats_kernel(const float* x, long ldx, int rows, int n, int group,
+                                                       float* stats, void* copy, int rmP, int rmn, int rmoff) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+  if (wave >= rows) return;  // whole waves leave together
+  const long row = rmP ? (long)(wave / rmP) * rmn + rmoff + wave % rmP : wave;
+  const int nc = n >> 2, parts = n / group;
+  for (int k = 0; k * 64 < nc; ++k) {
+    const int c = lane + 64 * k;
+    float s = 0.f, q = 0.f;
+    if (c < nc) {
+      const float4 v = ld4<float>(x, row * ldx + 4 * c);
+      s = (v.x + v.y) + (v.z + v.w);
+      q = (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+      if (copy) st4<TO>(copy, row * ldx + 4 * c, v);
+    }
+    s = dpp_add<0x140>(dpp_add<0x141>(dpp_add<0x4E>(dpp_add<0xB1>(s))));  // over the 16 lanes
+    q = dpp_add<0x140>(dpp_add<0x141>(dpp_add<0x4E>(dpp_add<0xB1>(q))));
+    if (group == 128) {  // lanes l and l ^ 16 hold the two halves of a 128-column group
+      s += __shfl_xor(s, 16);
+      q += __shfl_xor(q, 16);
+    }
+    const int g = (4 * c) / group;
+    if ((lane & (group / 4 - 1)) == 0 && c < nc) {
+      stats[(row * parts + g) * 2] = s;
+      stats[(row * parts + g) * 2 + 1] = q;
+    }
+  }
+}
+
+void ln_stats(const Exec& ex, const float* x, long ldx, int rows, int n, int group, float* stats, int copy_dt,
+              void* copy, int rm_P, int rm_n, int rm_off) {
+  SPLAT_CHECK(rows >= 0 && (group == 64 || group == 128) && n % group == 0 && ldx % 4 == 0 && in_dt_ok(copy_dt),
+              BAD_ARGUMENT, "ln_stats args");
+  SPLAT_CHECK((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(copy) & 15) == 0, BAD_ARGUMENT,
+              "ln_stats: 16-byte aligned rows");
+  if (ex.dry || rows == 0) return;
+  ProfScope ps(ex, "ln_stats", 0, double(rows) * n * (4 + (copy ? dtype_size(copy_dt) : 0)));
+  dim3 grid(cdiv(rows, 4));
+  if (copy_dt == F32) hipLaunchKernelGGL(ln_stats_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, rows, n, group, stats, copy, rm_P, rm_n, rm_off);
+  else hipLaunchKernelGGL(ln_stats_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, rows, n, group, stats, copy, rm_P, rm_n, rm_off);
+  SPLAT_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------
 // qk-norm + RoPE (depthanything3-rs/src/vit_block.rs:149-158 and rope.rs:57-73): one thread
 // per (row, head, q|k), in place on the qkv matrix.
 // q/k LayerNorm (64 channels, eps 1e-5) and 2D RoPE in place. 16 lanes per 64-channel vector

@@ -158,6 +158,32 @@ ConvT Loader::convt(const std::string& name, int cin, int cout, int s) {
   return ct;
 }
 
+Lin Loader::linear_ln(const std::string& name, int n_out, int n_in, const std::string& ln) {
+  auto w = host(name + ".weight", {n_out, n_in});
+  auto b = host(name + ".bias", {n_out});
+  const auto g = host(ln + ".weight", {n_in});
+  const auto beta = host(ln + ".bias", {n_in});
+  std::vector<float> c2(n_out);
+  std::vector<float> c1(n_out);
+  parallel_for(size_t(n_out), [&](size_t a, size_t e) {
+    for (size_t r = a; r < e; ++r) {
+      double sb = b[r], s1 = 0.0;
+      float* row = &w[r * size_t(n_in)];
+      for (int k = 0; k < n_in; ++k) {
+        sb += double(beta[k]) * row[k];
+        row[k] *= g[k];
+        s1 += dt_ == F32 ? double(row[k]) : double(bf2f(f2bf(row[k])));  // the stored value
+      }
+      c2[r] = float(sb);
+      c1[r] = float(s1);
+    }
+  });
+  float* bias = static_cast<float*>(ctx_.pool.upload(c2.data(), c2.size() * 4));
+  Lin l = pack(w, n_out, n_in, bias, dt_);
+  l.c1 = static_cast<float*>(ctx_.pool.upload(c1.data(), c1.size() * 4));
+  return l;
+}
+
 LN Loader::ln(const std::string& name, int n) {
   LN l;
   l.n = n;
@@ -173,20 +199,18 @@ Block Loader::block(const std::string& p, int dim, int hidden, bool swiglu, bool
   b.hidden = hidden;
   b.swiglu = swiglu;
   b.qk = qk;
-  b.n1 = ln(p + ".norm1", dim);
-  b.qkv = linear(p + ".attn.qkv", 3 * dim, dim);
+  b.qkv = linear_ln(p + ".attn.qkv", 3 * dim, dim, p + ".norm1");
   if (qk) {
     b.qn = ln(p + ".attn.q_norm", 64);
     b.kn = ln(p + ".attn.k_norm", 64);
   }
   b.proj = linear(p + ".attn.proj", dim, dim);
   b.ls1 = vec(p + ".ls1.gamma", {dim});
-  b.n2 = ln(p + ".norm2", dim);
   if (swiglu) {
-    b.fc1 = linear(p + ".mlp.w12", 2 * hidden, dim);
+    b.fc1 = linear_ln(p + ".mlp.w12", 2 * hidden, dim, p + ".norm2");
     b.fc2 = linear(p + ".mlp.w3", dim, hidden);
   } else {
-    b.fc1 = linear(p + ".mlp.fc1", hidden, dim);
+    b.fc1 = linear_ln(p + ".mlp.fc1", hidden, dim, p + ".norm2");
     b.fc2 = linear(p + ".mlp.fc2", dim, hidden);
   }
   b.ls2 = vec(p + ".ls2.gamma", {dim});
@@ -197,7 +221,12 @@ Block Loader::block(const std::string& p, int dim, int hidden, bool swiglu, bool
 
 void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, int hidden, bool swiglu) {
   const size_t es = dtype_size(dt);
-  s.h = ctx.arena.alloc(rows * dim * es);
+  SPLAT_CHECK(dim % 64 == 0, BAD_ARGUMENT, "transformer width must be a multiple of 64");
+  s.h = dt == F32 ? nullptr : ctx.arena.alloc(rows * dim * es);
+  s.ln_group = dim <= 1024 ? 64 : 128;  // at most 16 partials a row for the folded consumers
+  SPLAT_CHECK(dim % s.ln_group == 0 && dim / s.ln_group <= 16, BAD_ARGUMENT, "transformer width for the folded norms");
+  s.lnst = ctx.arena.alloc_t<float>(size_t(rows) * (dim / s.ln_group) * 2);
+  s.ln_src = nullptr;
   s.qkv = ctx.arena.alloc(rows * 3 * dim * es);
   s.att = ctx.arena.alloc(rows * dim * es);
   s.mid = ctx.arena.alloc(rows * hidden * es);
@@ -227,20 +256,36 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
     }
     ctx.arena.release(m);
   };
+  // The LayerNorms (eps 1e-6, vit_block.rs:15 / mapanything vit_block.rs:8) are folded into
+  // qkv and fc1: they read the residual rows before the norm (bf16 copy or fp32) and the row
+  // statistics that the previous residual epilogue wrote.
+  if (s.ln_src != in) block_ln_refresh(ctx, dt, in, int(rows), d, s);
+  const void* xin = dt == F32 ? static_cast<const void*>(in) : s.h;
+  auto fold = [&](GemmArgs& a, const Lin& l) {
+    a.ln_in = s.lnst;
+    a.ln_parts = d / s.ln_group;
+    a.ln_c1 = l.c1;
+    a.ln_eps = 1e-6f;
+  };
+  auto emit = [&](GemmArgs& a) {  // residual epilogue: statistics (and bf16 copy) of its rows
+    a.ln_out = s.lnst;
+    a.ln_group = s.ln_group;
+    a.ln_copy = dt == F32 ? nullptr : s.h;
+  };
   // norm1 -> qkv
-  layer_norm(ex, F32, in, d, dt, s.h, d, int(rows), d, b.n1.w, b.n1.b, 1e-6f);
   GemmArgs g;
   g.dt = dt;
   g.M = int(rows);
   g.N = 3 * d;
   g.K = d;
-  g.A = s.h;
+  g.A = xin;
   g.lda = d;
   g.W = b.qkv.w;
   g.ldw = b.qkv.ldw;
   g.bias = b.qkv.b;
   g.out = s.qkv;
   g.ldc = 3 * d;
+  fold(g, b.qkv);
   gemm(ex, g);
   if (b.qk || rope)
     qk_norm_rope(ex, dt, s.qkv, int(rows), d, b.qk ? b.qn.w : nullptr, b.qk ? b.qn.b : nullptr, b.qk ? b.kn.w : nullptr,
@@ -279,18 +324,20 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
   p.out = out;
   p.ldc = d;
   p.out_f32 = 1;
+  emit(p);
   gemm(ex, p);
   // out += ls2 * mlp(norm2(out))
-  layer_norm(ex, F32, out, d, dt, s.h, d, int(rows), d, b.n2.w, b.n2.b, 1e-6f);
+  const void* xmid = dt == F32 ? static_cast<const void*>(out) : s.h;
   GemmArgs f1;
   f1.dt = dt;
   f1.M = int(rows);
   f1.K = d;
-  f1.A = s.h;
+  f1.A = xmid;
   f1.lda = d;
   f1.W = b.fc1.w;
   f1.ldw = b.fc1.ldw;
   f1.bias = b.fc1.b;
+  fold(f1, b.fc1);
   if (b.swiglu) {
     f1.N = 2 * b.hidden;
     f1.out = s.x12;
@@ -322,7 +369,15 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
   f2.out = out;
   f2.ldc = d;
   f2.out_f32 = 1;
+  emit(f2);
   gemm(ex, f2);
+  s.ln_src = out;
+}
+
+void block_ln_refresh(Context& ctx, int dt, const float* x, int rows, int dim, BlockScratch& s, int rm_P, int rm_n,
+                      int rm_off) {
+  ln_stats(ctx.ex, x, dim, rows, dim, s.ln_group, s.lnst, dt, dt == F32 ? nullptr : s.h, rm_P, rm_n, rm_off);
+  s.ln_src = x;
 }
 
 // --- DPT building blocks --------------------------------------------------------------------

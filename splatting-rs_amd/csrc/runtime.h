@@ -56,6 +56,7 @@ struct Lin {
   long ldw = 0;
   int N = 0, K = 0, dt = BF16;
   float* b = nullptr;
+  float* c1 = nullptr;  // folded LayerNorm (Loader::linear_ln): sum_k w[n, k] of the stored weights
 };
 // Implicit-GEMM convolution weight [cout, ks*ks*cin] (k = (ky*ks + kx)*cin + ci).
 struct Conv {
@@ -72,10 +73,12 @@ struct LN {
   float* b = nullptr;
   int n = 0;
 };
+// A pre-norm block. norm1 is folded into qkv and norm2 into fc1 (Loader::linear_ln): they
+// consume the un-normalised residual rows and their statistics (GemmArgs::ln_in).
 struct Block {
   int dim = 0, heads = 0, hidden = 0;
   bool swiglu = false, qk = false;
-  LN n1, n2, qn, kn;
+  LN qn, kn;
   Lin qkv, proj, fc1, fc2;  // SwiGLU: fc1 = w12 (2*hidden outputs), fc2 = w3
   float* ls1 = nullptr;
   float* ls2 = nullptr;
@@ -93,6 +96,9 @@ class Loader {
   float* vec(const std::string& name, const std::vector<int64_t>& shape);
   std::vector<float> host(const std::string& name, const std::vector<int64_t>& shape);
   Block block(const std::string& name, int dim, int hidden, bool swiglu, bool qk);
+  // linear(LN(x)) with the LayerNorm `ln` (weight g, bias beta) folded in: weights w * g
+  // (along K), bias b + w beta, c1 = row sums of the stored (rounded) folded weights.
+  Lin linear_ln(const std::string& name, int n_out, int n_in, const std::string& ln);
   int dt() const { return dt_; }
   // Uploads row-major [n, k] host weights padded to a multiple of 64 columns, as `dt`.
   Lin pack(std::vector<float>& rows, int n, int k, float* bias, int dt);
@@ -117,8 +123,15 @@ struct Hooks {
 };
 
 // Scratch buffers of one transformer stack, sized for its largest block.
+// The LayerNorms folded into qkv / fc1 read `lnst`, the row statistics of `ln_src` (groups of
+// `ln_group` columns), and in bf16 mode `h`, its rows in bf16 (fp32 mode reads the residual
+// rows themselves). block_forward refreshes them when `in` is another buffer; a caller that
+// rewrites rows of ln_src in place must refresh those rows.
 struct BlockScratch {
-  void* h = nullptr;     // [rows, dim] normed input (dtype)
+  void* h = nullptr;     // [rows, dim] residual rows in bf16 (bf16 mode)
+  float* lnst = nullptr; // [rows, dim / ln_group, 2] (sum, sum of squares)
+  int ln_group = 64;
+  const float* ln_src = nullptr;
   void* qkv = nullptr;   // [rows, 3*dim]
   void* att = nullptr;   // [rows, dim]
   void* mid = nullptr;   // [rows, hidden]
@@ -134,6 +147,10 @@ void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, in
 // the block for the context's branch taps.
 void block_forward(Context& ctx, const Block& b, int dt, const float* in, float* out, long rows, int seqs, int L,
                    BlockScratch& s, int rope, int n, int cols, const float* rope_table, int npos, int block);
+// Recomputes the row statistics (and the bf16 copy) of `rows` rows of x (row r at
+// (r / rm_P) * rm_n + rm_off + r % rm_P when rm_P > 0) and makes x the scratch's ln_src.
+void block_ln_refresh(Context& ctx, int dt, const float* x, int rows, int dim, BlockScratch& s, int rm_P = 0,
+                      int rm_n = 0, int rm_off = 0);
 
 // GEMM arguments of a convolution on an NHWC map [V, Hi, Wi, cin]: ks == 1 -> plain rows,
 // ks == 3 -> implicit im2col with padding 1. The caller adds epilogue fields.

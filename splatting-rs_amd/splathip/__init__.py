@@ -103,6 +103,11 @@ SIGNATURES = {
     "splat_ma_encode_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "splat_kernel_gemm": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int,
                                     C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
+    "splat_kernel_gemm_ln": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
+                                       C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_float, C.c_void_p,
+                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
+    "splat_kernel_ln_stats": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int,
+                                        C.c_void_p]),
     "splat_kernel_attention": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "splat_kernel_attention_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
                                                  C.c_int]),
@@ -350,6 +355,19 @@ class Context:
                     out: int, out_f32: bool):
         self.check(self._lib.splat_kernel_gemm(self.handle, dtype, C.c_void_p(A), M, K, C.c_void_p(W), N, ldw,
                                                C.c_void_p(bias), act, C.c_void_p(out), int(out_f32)))
+
+    def kernel_gemm_ln(self, dtype: int, A: int, M: int, K: int, W: int, N: int, ldw: int, bias: int, act: int,
+                       out: int, out_f32: bool, ln_in: int = 0, c1: int = 0, eps: float = 1e-6, gamma: int = 0,
+                       res: int = 0, ln_out: int = 0, copy: int = 0, group: int = 64):
+        """splat_kernel_gemm_ln (device pointers as ints, 0 for NULL)."""
+        v = lambda p: C.c_void_p(p or None)
+        self.check(self._lib.splat_kernel_gemm_ln(self.handle, dtype, v(A), M, K, v(W), N, ldw, v(bias), act, v(ln_in),
+                                                  v(c1), eps, v(gamma), v(res), v(ln_out), v(copy), group, v(out),
+                                                  int(out_f32)))
+
+    def kernel_ln_stats(self, x: int, rows: int, n: int, group: int, stats: int, dtype: int, copy: int = 0):
+        self.check(self._lib.splat_kernel_ln_stats(self.handle, C.c_void_p(x), rows, n, group, C.c_void_p(stats),
+                                                   dtype, C.c_void_p(copy or None)))
 
     def kernel_attention(self, dtype: int, qkv: int, out: int, S: int, L: int, heads: int):
         self.check(self._lib.splat_kernel_attention(self.handle, dtype, C.c_void_p(qkv), C.c_void_p(out), S, L, heads))

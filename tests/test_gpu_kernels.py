@@ -273,3 +273,133 @@ def test_resize_bilinear_matches_torch(ctx, dtype, V, Hi, Wi, C, Ho, Wo):
     got = out.cpu().double().permute(0, 3, 1, 2)
     err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
     assert err < (1e-6 if dtype == "f32" else 8e-3), err
+
+
+# --- LayerNorm folded into the block GEMMs (GemmArgs::ln_in / ln_out) ----------------------
+
+def _group_sums(x, group):
+    """(sum, sum of squares) of fp32 rows per group of columns, fp64: [M, K/group, 2]."""
+    M, K = x.shape
+    g = x.double().reshape(M, K // group, group)
+    return torch.stack([g.sum(-1), (g * g).sum(-1)], -1)
+
+
+LN_CONSUMER_CASES = [
+    # (M, N, K, act, group): qkv (act 0) and fc1 (act 2) shapes of the networks and the tiles they take
+    (6222, 3072, 1024, 0, 64),   # MapAnything encoder qkv: 320x256 tiles
+    (6222, 4096, 1024, 2, 64),   # encoder fc1 (GELU): 256x256
+    (6223, 2304, 768, 0, 64),    # info-sharing qkv: 256x256
+    (6223, 3072, 768, 2, 64),    # info-sharing fc1: 320x256
+    (5838, 1152, 384, 0, 64),    # DA3-Small C2 qkv
+    (1297, 1536, 384, 2, 64),    # DA3-Small C1 fc1
+    (2074, 3072, 1024, 0, 64),   # MapAnything C3 encoder qkv
+    (1400, 4608, 1536, 0, 128),  # reference-dims MapAnything qkv (128-column groups)
+    (100, 256, 1024, 1, 64),     # would split K: runs unsplit (a row's statistics need all of K); ragged rows
+    (333, 640, 192, 0, 64),      # 128-row tiles, ragged rows, three partials a row
+    (64, 64, 64, 0, 64),         # one tile, one k-tile, one partial
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("M,N,K,act,group", LN_CONSUMER_CASES)
+def test_gemm_folded_layernorm_matches_torch(ctx, dtype, M, N, K, act, group):
+    """act(LN(x) W^T + b) from the un-normalised rows, their statistics (ln_stats kernel) and the
+    folded weights, rows with a non-zero mean so that the mean term matters: (1) the epilogue
+    algebra against fp64 on the same rounded operands; (2) the whole fold against torch's
+    LayerNorm and linear in fp64 (bf16: the rounding of x and of W * gamma)."""
+    report("gemm_ln", dtype=dtype, M=M, N=N, K=K, act=act, group=group)
+    code, tdt = _dt(dtype)
+    g = torch.Generator().manual_seed(M + 5 * N + 11 * K)
+    x = torch.randn(M, K, generator=g) + 0.7 * torch.randn(M, 1, generator=g)
+    gamma = 1 + 0.2 * torch.randn(K, generator=g)
+    beta = 0.1 * torch.randn(K, generator=g)
+    Wl = torch.randn(N, K, generator=g) * 0.05
+    bl = torch.randn(N, generator=g) * 0.1
+    Wf = (Wl * gamma).to(tdt)           # folded, as stored
+    c1 = Wf.double().sum(1).float()
+    c2 = (bl.double() + Wl.double() @ beta.double()).float()
+    ldw = (K + 63) // 64 * 64
+    Wp = torch.zeros(N, ldw, dtype=tdt)
+    Wp[:, :K] = Wf
+    dx = x.cuda()
+    stats = torch.empty(M, K // group, 2, device="cuda")
+    copy = torch.empty(M, K, dtype=tdt, device="cuda") if dtype == "bf16" else None
+    dW, dc1, dc2 = Wp.cuda(), c1.cuda(), c2.cuda()
+    out = torch.empty(M, N, device="cuda")
+    torch.cuda.synchronize()
+    ctx.kernel_ln_stats(dx.data_ptr(), M, K, group, stats.data_ptr(), code, copy.data_ptr() if copy is not None else 0)
+    A = copy if copy is not None else dx
+    ctx.kernel_gemm_ln(code, A.data_ptr(), M, K, dW.data_ptr(), N, ldw, dc2.data_ptr(), act, out.data_ptr(), True,
+                       ln_in=stats.data_ptr(), c1=dc1.data_ptr(), eps=1e-6, group=group)
+    ctx.synchronize()
+    st = stats.cpu().double()
+    ref_st = _group_sums(x, group)
+    assert torch.allclose(st, ref_st, rtol=1e-5, atol=1e-3), (st - ref_st).abs().max()
+    if copy is not None:
+        assert torch.equal(copy.cpu(), x.to(tdt))
+    # (1) same operands: rstd * (x~ Wf^T - mean c1) + c2, statistics of the fp32 rows
+    mean = ref_st[:, :, 0].sum(1, keepdim=True) / K
+    rstd = 1 / torch.sqrt(ref_st[:, :, 1].sum(1, keepdim=True) / K - mean * mean + 1e-6)
+    xs = x.to(tdt).double()
+    act_fn = {0: lambda t: t, 1: torch.relu, 2: torch.nn.functional.gelu}[act]
+    ref = act_fn(rstd * (xs @ Wf.double().T - mean * c1.double()[None]) + c2.double())
+    got = out.cpu().double()
+    err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
+    # (2) the fold against LayerNorm -> linear
+    true = act_fn(torch.nn.functional.layer_norm(x.double(), (K,), gamma.double(), beta.double(), 1e-6)
+                  @ Wl.double().T + bl.double())
+    err2 = (got - true).abs().max().item() / (true.abs().max().item() + 1e-12)
+    report("gemm_ln.err", same_operands=f"{err:.2e}", vs_layer_norm=f"{err2:.2e}")
+    assert err < 2e-5, err
+    assert err2 < (1e-5 if dtype == "f32" else 2e-2), err2
+
+
+LN_PRODUCER_CASES = [
+    # (M, N, K, group): proj / fc2 residual epilogues
+    (6222, 1024, 1024, 64),   # MapAnything encoder proj: 256x128 tiles
+    (6222, 1024, 4096, 64),   # encoder fc2
+    (6223, 768, 768, 64),     # info proj: 192x128 tiles (32-column waves: sums meet in LDS)
+    (6223, 768, 3072, 64),    # info fc2
+    (5838, 384, 1536, 64),    # DA3-Small C2 fc2: 128x128 tiles
+    (1297, 384, 1536, 64),    # DA3-Small C1 fc2: split-K, statistics from the ln_stats kernel
+    (1400, 1536, 1536, 128),  # reference-dims MapAnything proj (128-column groups)
+    (200, 128, 64, 64),       # one row tile, ragged
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("M,N,K,group", LN_PRODUCER_CASES)
+def test_gemm_residual_statistics(ctx, dtype, M, N, K, group):
+    """out = res + gamma * (A W^T + b) in fp32, the (sum, sum of squares) of every output row per
+    group of columns, and the output rows in the GEMM's dtype, bit for bit the stored rows rounded."""
+    report("gemm_resln", dtype=dtype, M=M, N=N, K=K, group=group)
+    code, tdt = _dt(dtype)
+    g = torch.Generator().manual_seed(3 * M + N + 7 * K)
+    A = torch.randn(M, K, generator=g).to(tdt)
+    ldw = (K + 63) // 64 * 64
+    Wm = torch.zeros(N, ldw)
+    Wm[:, :K] = torch.randn(N, K, generator=g) * 0.05
+    Wm = Wm.to(tdt)
+    bias = torch.randn(N, generator=g)
+    gam = torch.rand(N, generator=g) + 0.5
+    res = torch.randn(M, N, generator=g)
+    dA, dW, db, dg, dr = A.cuda(), Wm.cuda(), bias.cuda(), gam.cuda(), res.cuda()
+    out = torch.empty(M, N, device="cuda")
+    stats = torch.full((M, N // group, 2), float("nan"), device="cuda")
+    copy = torch.empty(M, N, dtype=tdt, device="cuda")
+    torch.cuda.synchronize()
+    ctx.kernel_gemm_ln(code, dA.data_ptr(), M, K, dW.data_ptr(), N, ldw, db.data_ptr(), 0, out.data_ptr(), True,
+                       gamma=dg.data_ptr(), res=dr.data_ptr(), ln_out=stats.data_ptr(), copy=copy.data_ptr(),
+                       group=group)
+    ctx.synchronize()
+    ref = res.double() + gam.double() * (A.double() @ Wm[:, :K].double().T + bias.double())
+    got = out.cpu()
+    err = (got.double() - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
+    st = stats.cpu().double()
+    ref_st = _group_sums(got, group)  # the statistics are of the stored fp32 outputs
+    scale = _group_sums(got.abs(), group)
+    st_err = ((st - ref_st).abs() / (scale + 1e-6)).max().item()
+    report("gemm_resln.err", out=f"{err:.2e}", stats=f"{st_err:.2e}")
+    assert err < (1e-5 if dtype == "f32" else 2e-5), err
+    assert st_err < 1e-5, st_err
+    assert torch.equal(copy.cpu(), got.to(tdt))
