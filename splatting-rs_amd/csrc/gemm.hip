@@ -225,12 +225,100 @@ __device__ __forceinline__ void read8(const float* q, float* v) {
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-// `lnab` (EPI_LN): (rstd, -rstd * mean) of this wave's rows in LDS. `lnp` (EPI_RESLN): this
-// wave's corner of the LDS array of 32-column sums, lnp_ld a row.
+// qk-norm + RoPE (GemmArgs::qk_dim) of a wave's column runs n..n+7 in CH rows (q or k columns,
+// heads 64-column aligned). Channel c0 = n % 64. The head's statistics: with RUNS >= 8 lanes a
+// row (waves 64+ columns wide) the 8 lanes of a head reduce them by DPP; with RUNS = 4 (32-column
+// waves) each half-head's (sum, sum of squares) meets the other half's in LDS (`xch`, two pairs
+// per tile row) across a block barrier. The RoPE partner of channel c (c +- 16 in its 32-channel
+// half) is in lane ^ 2 (quad_perm [2,3,0,1]). Every lane of the block calls it, also for v
+// columns (`qk` false), so that the barrier is uniform.
+template <int RUNS, int CH>
+__device__ inline void qk_norm_rope(const GemmArgs& p, float (&v)[CH][8], const long (&m)[CH], long n, int lane,
+                                    bool qk, float* xch, const int (&xrow)[CH]) {
+  const int c0 = int(n % 64);
+  const bool isk = n >= p.qk_dim;
+  const float* w = isk ? p.kw : p.qw;
+  const float* b = isk ? p.kb : p.qb;
+  if (p.qw) {  // LayerNorm over each head's 64 channels (eps 1e-5, vit_block.rs:17)
+    float mean[CH], rstd[CH];
+    if constexpr (RUNS >= 8) {
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s += v[t][k];
+        mean[t] = group_sum<8>(s) * (1.f / 64.f);
+        float q = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q = fmaf(v[t][k] - mean[t], v[t][k] - mean[t], q);
+        rstd[t] = rsqrtf(group_sum<8>(q) * (1.f / 64.f) + 1e-5f);
+      }
+    } else {
+      const int half = c0 >> 5;
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        float s = 0.f, q = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          s += v[t][k];
+          q = fmaf(v[t][k], v[t][k], q);
+        }
+        s = group_sum<4>(s);
+        q = group_sum<4>(q);
+        if ((lane & 3) == 0 && qk) {
+          xch[(xrow[t] * 2 + half) * 2] = s;
+          xch[(xrow[t] * 2 + half) * 2 + 1] = q;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        const float* e = xch + xrow[t] * 4;
+        const float s = e[0] + e[2], q = e[1] + e[3];
+        mean[t] = s * (1.f / 64.f);
+        rstd[t] = rsqrtf(fmaxf(q * (1.f / 64.f) - mean[t] * mean[t], 0.f) + 1e-5f);
+      }
+      __syncthreads();  // the exchange area is reused by the next slab
+    }
+    if (qk) {
+#pragma unroll
+      for (int t = 0; t < CH; ++t)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[t][k] = (v[t][k] - mean[t]) * rstd[t] * w[c0 + k] + b[c0 + k];
+    }
+  }
+  if (p.rope_cs && qk) {
+    const bool first = (c0 & 16) == 0;  // channel c < 16 of its half: pairs with c + 16
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+      const long tok = m[t] % p.rope_n;
+      int pr = 0, pc = 0;
+      if (tok > 0) {
+        if (p.rope_across) pr = pc = 1;
+        else {
+          pr = int((tok - 1) / p.rope_cols) + 1;
+          pc = int((tok - 1) % p.rope_cols) + 1;
+        }
+      }
+      const int pos = c0 >= 32 ? pc : pr;  // channels 32-63 rotate by the column position
+      const float* cs = p.rope_cs + pos * 16 + (c0 & 8);
+      const float* sn = p.rope_cs + (p.rope_npos + pos) * 16 + (c0 & 8);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float pv = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[t][k]), 0x4E, 0xf, 0xf, true));
+        v[t][k] = first ? v[t][k] * cs[k] - pv * sn[k] : v[t][k] * cs[k] + pv * sn[k];
+      }
+    }
+  }
+}
+
+// `lnab` (EPI_LN): (rstd, -rstd * mean) of this wave's rows in LDS; `xch` (EPI_LN with
+// qk_dim): the block's qk-norm exchange area, xrow0 this wave's first tile row. `lnp`
+// (EPI_RESLN): this wave's corner of the LDS array of 32-column sums, lnp_ld a row.
 template <typename T, int TM, int TN, int EPI>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long wrow0, long wcol0, float* slab,
                                          int lane, bool vec, float* part = nullptr, const float* lnab = nullptr,
-                                         float* lnp = nullptr, int lnp_ld = 0) {
+                                         float* lnp = nullptr, int lnp_ld = 0, float* xch = nullptr, int xrow0 = 0) {
   constexpr int COLS = TN * 32, LD = slab_ld(TN), RUNS = COLS / 8;
   if constexpr (EPI == EPI_PART) {
     // rows of 8 columns: n < N implies n + 8 <= ldp (ldp is N rounded up to 8)
@@ -314,8 +402,6 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
         }
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
-          const int rr = rsub + (t0 + t) * (64 / RUNS);
-          const long m = wrow0 + i * 32 + rr;
           float* x = v[t];
           if constexpr (EPI == EPI_LN) {
 #pragma unroll
@@ -331,6 +417,25 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
 #pragma unroll
             for (int k = 0; k < 8; ++k) x[k] = gelu_erf(x[k]);
           }
+        }
+        if constexpr (EPI == EPI_LN) {
+          if (p.qk_dim) {  // block-uniform (a barrier inside for 32-column waves)
+            static_assert(EPI != EPI_LN || CH == IT, "qk-norm: a slab's rows in one chunk");
+            long mm[CH];
+            int xr[CH];
+#pragma unroll
+            for (int t = 0; t < CH; ++t) {
+              xr[t] = xrow0 + i * 32 + rsub + (t0 + t) * (64 / RUNS);
+              mm[t] = wrow0 + i * 32 + rsub + (t0 + t) * (64 / RUNS);
+            }
+            qk_norm_rope<RUNS, CH>(p, v, mm, n, lane, wcol0 < 2 * p.qk_dim, xch, xr);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+          const int rr = rsub + (t0 + t) * (64 / RUNS);
+          const long m = wrow0 + i * 32 + rr;
+          float* x = v[t];
           if (RES) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) x[k] *= cg[k];
@@ -662,6 +767,8 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   static_assert((STAGES - 1) * LPT <= 63, "vmcnt range");
   static_assert(STAGES * STAGE >= NW * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the ring");
   static_assert(EPI != EPI_LN || NW * 64 >= BM, "folded LayerNorm: a thread per tile row");
+  static_assert(EPI != EPI_LN || STAGES * STAGE >= (NW * 32 * slab_ld(TN) + (WN + 1) / 2 * BM * 4) * 4,
+                "qk-norm exchange past the epilogue slabs");
   static_assert(EPI != EPI_RESLN || STAGES * STAGE >= (NW * 32 * slab_ld(TN) + BM * (BN / 32) * 2) * 4,
                 "row statistics: the 32-column sums past the epilogue slabs");
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
@@ -941,7 +1048,8 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
     float* lnp = reinterpret_cast<float*>(smem) + NW * 32 * slab_ld(TN);
     epilogue<T, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
                              EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr, lnab + wm * (BM / WM) * 2,
-                             lnp + (wm * (BM / WM) * LNLD + wn * (BN / WN) / 32) * 2, LNLD);
+                             lnp + (wm * (BM / WM) * LNLD + wn * (BN / WN) / 32) * 2, LNLD,
+                             lnp + (wn / 2) * BM * 4, wm * (BM / WM));
     if constexpr (EPI == EPI_RESLN) {
       // every wave's 32-column sums are in LDS: one (sum, sum of squares) per row and group
       __syncthreads();
@@ -1090,8 +1198,8 @@ static BfCfg pick_bf16(const GemmArgs& a) {
   // Narrow outputs (the DA3 head's 32/64-channel convs): 128-row tiles and two stages keep the
   // LDS per block at 40-48 KB, so 3-4 blocks share a CU and hide each other's load latency
   // (C2 convs 475 -> 266 us against 256-row tiles with 3-4 stages).
-  if (a.N <= 32) return CFG_128x32;
-  if (a.N <= 64) return CFG_128x64;
+  if (a.N <= 32 && !a.qk_dim) return CFG_128x32;
+  if (a.N <= 64 && !a.qk_dim) return CFG_128x64;
   // 128-channel convolutions over many tiles (the DPT heads' output convs at full and half
   // resolution): 192x128 tiles with two stages, 80 KB of LDS, so that two blocks share a CU and
   // one block's prologue and epilogue overlap the other's main loop. Measured from 1.5 rounds of
@@ -1136,8 +1244,8 @@ static size_t split_bytes(const GemmArgs& a, int S) {
 // operand traffic is minor and the tile choice only has to fill the CUs: a round of resident
 // tiles runs per_cu tiles per CU side by side, so its cost is per_cu x the tile's area.
 static BfCfg pick_f32(const GemmArgs& a) {
-  if (a.N <= 32) return CFG_128x32;
-  if (a.N <= 64) return CFG_F64x64;
+  if (a.N <= 32 && !a.qk_dim) return CFG_128x32;
+  if (a.N <= 64 && !a.qk_dim) return CFG_F64x64;
   const BfCfg cands[] = {CFG_256x256, CFG_256x128, CFG_F128x128, CFG_F64x64};
   double best = 1e30;
   BfCfg pick = CFG_256x256;
@@ -1245,6 +1353,13 @@ void gemm(const Exec& ex, const GemmArgs& args) {
                     !a.gamma && !a.res2 && !a.addtab && !a.rm_P && !a.act_post && a.store == STORE_ROWS && a.epi_vec,
                 BAD_ARGUMENT, "gemm: a folded LayerNorm needs plain aligned rows, a bias/activation epilogue and "
                               "at most 16 partials a row");
+  if (a.qk_dim)
+    SPLAT_CHECK(a.ln_in && a.N == 3 * a.qk_dim && a.qk_dim % 64 == 0 && (a.qw == nullptr) == (a.qb == nullptr) &&
+                    (a.kw == nullptr) == (a.kb == nullptr) && (!a.rope_cs || (a.rope_n > 0 && a.rope_cols > 0)),
+                BAD_ARGUMENT, "gemm: qk-norm + RoPE need a folded-LayerNorm qkv GEMM");
+  if (a.rope_cs && !a.rope_across && a.qk_dim)
+    SPLAT_CHECK((a.rope_n - 1) / a.rope_cols + 1 < a.rope_npos && a.rope_cols + 1 <= a.rope_npos, BAD_ARGUMENT,
+                "gemm: RoPE table too small");
   if (a.ln_out)
     SPLAT_CHECK((a.ln_group == 64 || a.ln_group == 128) && a.N % a.ln_group == 0 && a.out_f32 &&
                     a.store == STORE_ROWS && !a.rm_P && a.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&

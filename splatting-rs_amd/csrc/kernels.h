@@ -65,6 +65,17 @@ struct GemmArgs {
   //   residual, remap or table) and runs without split-K.
   float* ln_out = nullptr; int ln_group = 64; void* ln_copy = nullptr;
   const float* ln_in = nullptr; int ln_parts = 0; const float* ln_c1 = nullptr; float ln_eps = 0.f;
+  // qk-norm + 2D RoPE of a DA3 qkv GEMM (depthanything3-rs/src/vit_block.rs:155-162,
+  // rope.rs:57-73), applied to the q and k columns in the epilogue (qk_dim = d > 0, N = 3 d,
+  // heads of 64 columns, needs a folded-LayerNorm consumer): per head LayerNorm over its 64
+  // channels (eps 1e-5; qw/qb, kw/kb [64], null: no norm), then with rope_cs != null the
+  // rotation of channel pairs (c, c + 16) within each 32-channel half, channels 0-31 by the
+  // token's row position and 32-63 by its column position; rope_cs [npos][16] cos then
+  // [npos][16] sin. Token t = m % rope_n: t = 0 at (0, 0), patch t at ((t-1) / rope_cols + 1,
+  // (t-1) % rope_cols + 1), or (1, 1) with rope_across.
+  int qk_dim = 0; const float* qw = nullptr; const float* qb = nullptr; const float* kw = nullptr;
+  const float* kb = nullptr; const float* rope_cs = nullptr; int rope_n = 1, rope_cols = 1, rope_across = 0,
+  rope_npos = 0;
 };
 // A producer whose tile path cannot emit the statistics (split-K, unaligned, tiles narrower
 // than the group) gets them (and the copy) from ln_stats() on its output.
@@ -106,13 +117,6 @@ void* attention_scratch(int device);
 void layer_norm(const Exec& ex, int in_dt, const void* in, long ldin, int out_dt, void* out, long ldout,
                 int rows, int n, const float* w, const float* b, float eps, int rm_P = 0, int rm_n = 0,
                 int rm_off = 0);
-
-// Per-head LayerNorm (64 ch, eps 1e-5) of q and k inside a [rows, 3*dim] qkv matrix, then 2D
-// RoPE. Token t's position: tok = t % n; tok 0 -> (0,0); patches -> (p/cols+1, p%cols+1)
-// (within a view) or (1,1) (across views). cs: [npos][16] cos then [npos][16] sin.
-void qk_norm_rope(const Exec& ex, int dt, void* qkv, int rows, int dim, const float* qw, const float* qb,
-                  const float* kw, const float* kb, int n, int cols, int across, const float* cs, int npos,
-                  int rope);
 
 // images fp32 [V,3,H,W] -> patch matrix [V*R*C, kpad] (dtype dt), k = c*196 + ky*14 + kx.
 void im2col_patch(const Exec& ex, int dt, const float* img, int V, int H, int W, void* out, int kpad);

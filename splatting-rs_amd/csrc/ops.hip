@@ -1,4 +1,4 @@
-// HBM-bound and small kernels around the GEMMs and attention: LayerNorms, qk-norm + 2D RoPE,
+// HBM-bound and small kernels around the GEMMs and attention: LayerNorms, row statistics,
 // patch im2col, bilinear resize (align_corners=True), DPT output heads, small head linears,
 // DA3 reference-view selection and hook assembly, and elementwise helpers.
 #include "kernels.h"
@@ -205,81 +205,6 @@ void ln_stats(const Exec& ex, const float* x, long ldx, int rows, int n, int gro
   dim3 grid(cdiv(rows, 4));
   if (copy_dt == F32) hipLaunchKernelGGL(ln_stats_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, rows, n, group, stats, copy, rm_P, rm_n, rm_off);
   else hipLaunchKernelGGL(ln_stats_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, rows, n, group, stats, copy, rm_P, rm_n, rm_off);
-  SPLAT_HIP(hipGetLastError());
-}
-
-// ---------------------------------------------------------------------------------------
-// qk-norm + RoPE (depthanything3-rs/src/vit_block.rs:149-158 and rope.rs:57-73): one thread
-// per (row, head, q|k), in place on the qkv matrix.
-// q/k LayerNorm (64 channels, eps 1e-5) and 2D RoPE in place. 16 lanes per 64-channel vector
-// (one head of q or of k of one row), 4 consecutive channels a lane: every vector is one
-// 128-byte access, its statistics a 16-lane DPP sum, and the RoPE pair of channel c (c +- 16
-// within its 32-channel axis half) sits in lane j ^ 4 at the same position.
-template <typename T>
-__global__ void __launch_bounds__(256) qk_kernel(void* qkv, int rows, int dim, const float* qw, const float* qb,
-                                                 const float* kw, const float* kb, int n, int cols, int across,
-                                                 const float* cs, int npos, int rope) {
-  const int heads = dim / 64;
-  const long vid = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int j = threadIdx.x & 15;
-  if (vid >= (long)rows * heads * 2) return;  // whole 16-lane groups leave together
-  const int which = int(vid & 1);
-  const long rh = vid >> 1;
-  const long row = rh / heads;
-  const int h = int(rh - row * heads);
-  T* x = reinterpret_cast<T*>(qkv) + row * 3L * dim + which * dim + h * 64 + 4 * j;
-  const float4 f = ld4<T>(x, 0);
-  float v[4] = {f.x, f.y, f.z, f.w};
-  const float* w = which ? kw : qw;
-  const float* b = which ? kb : qb;
-  if (w) {
-    float s = (v[0] + v[1]) + (v[2] + v[3]);
-    s = dpp_add<0x140>(dpp_add<0x141>(dpp_add<0x4E>(dpp_add<0xB1>(s))));  // over the 16 lanes
-    const float mean = s * (1.f / 64.f);
-    float q = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float d = v[k] - mean;
-      q += d * d;
-    }
-    q = dpp_add<0x140>(dpp_add<0x141>(dpp_add<0x4E>(dpp_add<0xB1>(q))));
-    const float rstd = rsqrtf(q * (1.f / 64.f) + 1e-5f);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = (v[k] - mean) * rstd * w[4 * j + k] + b[4 * j + k];
-  }
-  if (rope) {
-    const int tok = int(row % n);
-    int pr = 0, pc = 0;
-    if (tok > 0) {
-      if (across) { pr = 1; pc = 1; }
-      else { pr = (tok - 1) / cols + 1; pc = (tok - 1) % cols + 1; }
-    }
-    // channels 0-31 rotate by the row position, 32-63 by the column position; channel c of a
-    // half pairs with c + 16 (lanes j with j & 4 == 0 hold the first of the pair)
-    const int pos = (j >> 3) ? pc : pr;
-    const float* cosr = cs + (long)pos * 16 + 4 * (j & 3);
-    const float* sinr = cs + (long)npos * 16 + (long)pos * 16 + 4 * (j & 3);
-    const bool first = (j & 4) == 0;
-    float pv[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) pv[k] = __shfl_xor(v[k], 4, 16);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = first ? v[k] * cosr[k] - pv[k] * sinr[k] : v[k] * cosr[k] + pv[k] * sinr[k];
-  }
-  st4<T>(x, 0, make_float4(v[0], v[1], v[2], v[3]));
-}
-
-void qk_norm_rope(const Exec& ex, int dt, void* qkv, int rows, int dim, const float* qw, const float* qb,
-                  const float* kw, const float* kb, int n, int cols, int across, const float* cs, int npos, int rope) {
-  SPLAT_CHECK(dim % 64 == 0 && n > 0 && cols > 0, BAD_ARGUMENT, "qk_norm_rope args");
-  SPLAT_CHECK(!rope || cs != nullptr, BAD_ARGUMENT, "qk_norm_rope: missing rope table");
-  if (rope && !across) SPLAT_CHECK((n - 1) / cols + 1 < npos && cols + 1 <= npos, BAD_ARGUMENT, "rope table too small");
-  if (ex.dry || rows == 0) return;
-  ProfScope ps(ex, "qk_norm_rope", 0, 4.0 * rows * dim * dtype_size(dt));
-  const long vectors = (long)rows * (dim / 64) * 2;  // 16 lanes each
-  dim3 grid(unsigned(cdiv(vectors, 16)));
-  if (dt == F32) hipLaunchKernelGGL(qk_kernel<float>, grid, dim3(256), 0, ex.stream, qkv, rows, dim, qw, qb, kw, kb, n, cols, across, cs, npos, rope);
-  else hipLaunchKernelGGL(qk_kernel<bf16>, grid, dim3(256), 0, ex.stream, qkv, rows, dim, qw, qb, kw, kb, n, cols, across, cs, npos, rope);
   SPLAT_HIP(hipGetLastError());
 }
 

@@ -286,10 +286,23 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
   g.out = s.qkv;
   g.ldc = 3 * d;
   fold(g, b.qkv);
+  if (b.qk || rope) {  // qk-norm + RoPE in the epilogue (vit_block.rs:155-162)
+    g.qk_dim = d;
+    if (b.qk) {
+      g.qw = b.qn.w;
+      g.qb = b.qn.b;
+      g.kw = b.kn.w;
+      g.kb = b.kn.b;
+    }
+    if (rope) {
+      g.rope_cs = rope_table;
+      g.rope_n = n;
+      g.rope_cols = cols;
+      g.rope_across = rope == 2;
+      g.rope_npos = npos;
+    }
+  }
   gemm(ex, g);
-  if (b.qk || rope)
-    qk_norm_rope(ex, dt, s.qkv, int(rows), d, b.qk ? b.qn.w : nullptr, b.qk ? b.qn.b : nullptr, b.qk ? b.kn.w : nullptr,
-                 b.qk ? b.kn.b : nullptr, n, cols, rope == 2, rope_table, npos, rope != 0);
   // attention
   AttnArgs a;
   a.dt = dt;
