@@ -156,7 +156,7 @@ void Da3Model::forward(const float* images, int V, int H, int W, const splat_da3
   }
   const size_t mark = ar.mark();
   BlockScratch s;
-  block_scratch(ctx_, s, dt_, T, d, spec_.hidden(), spec_.swiglu);
+  block_scratch(ctx_, s, dt_, T, d, spec_.hidden());
   float* cur = X0;
   float* within = X0;
   const int sel_at = std::max(spec_.alt_start - 1, 0);

@@ -431,6 +431,25 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
             qk_norm_rope<RUNS, CH>(p, v, mm, n, lane, wcol0 < 2 * p.qk_dim, xch, xr);
           }
         }
+        if constexpr (EPI == EPI_LN) {
+          if (p.glu) {
+            // SwiGLU: even runs hold x1 channels 8j..8j+7, the next lane's run the matching x2
+            // ones; the even lane stores silu(x1) * x2 at output column n / 2
+#pragma unroll
+            for (int t = 0; t < CH; ++t) {
+              const int rr = rsub + (t0 + t) * (64 / RUNS);
+              const long m = wrow0 + i * 32 + rr;
+              float y[8];
+#pragma unroll
+              for (int k = 0; k < 8; ++k) {
+                const float x2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[t][k]), 0xB1, 0xf, 0xf, true));
+                y[k] = v[t][k] / (1.f + __expf(-v[t][k])) * x2;
+              }
+              if (nok && m < p.M && (lane & 1) == 0) store8<T>(p, y, m * p.ldc + n / 2);
+            }
+            continue;
+          }
+        }
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
           const int rr = rsub + (t0 + t) * (64 / RUNS);
@@ -1353,6 +1372,9 @@ void gemm(const Exec& ex, const GemmArgs& args) {
                     !a.gamma && !a.res2 && !a.addtab && !a.rm_P && !a.act_post && a.store == STORE_ROWS && a.epi_vec,
                 BAD_ARGUMENT, "gemm: a folded LayerNorm needs plain aligned rows, a bias/activation epilogue and "
                               "at most 16 partials a row");
+  if (a.glu)
+    SPLAT_CHECK(a.ln_in && a.N % 16 == 0 && !a.qk_dim && a.act == ACT_NONE && a.ldc >= a.N / 2, BAD_ARGUMENT,
+                "gemm: the SwiGLU gate needs a folded-LayerNorm w12 GEMM with interleaved rows");
   if (a.qk_dim)
     SPLAT_CHECK(a.ln_in && a.N == 3 * a.qk_dim && a.qk_dim % 64 == 0 && (a.qw == nullptr) == (a.qb == nullptr) &&
                     (a.kw == nullptr) == (a.kb == nullptr) && (!a.rope_cs || (a.rope_n > 0 && a.rope_cols > 0)),

@@ -73,6 +73,11 @@ struct GemmArgs {
   // token's row position and 32-63 by its column position; rope_cs [npos][16] cos then
   // [npos][16] sin. Token t = m % rope_n: t = 0 at (0, 0), patch t at ((t-1) / rope_cols + 1,
   // (t-1) % rope_cols + 1), or (1, 1) with rope_across.
+  // SwiGLU gate of a w12 GEMM (mapanything-rs/src/vit_block.rs:64-70) in the epilogue (needs a
+  // folded-LayerNorm consumer): W rows (and bias) interleaved in chunks of 8, x1 rows 8j..8j+7
+  // then the matching x2 rows (Loader::linear_ln), N = 2 * hidden; out [M, ldc] holds
+  // silu(x1) * x2, hidden columns.
+  int glu = 0;
   int qk_dim = 0; const float* qw = nullptr; const float* qb = nullptr; const float* kw = nullptr;
   const float* kb = nullptr; const float* rope_cs = nullptr; int rope_n = 1, rope_cols = 1, rope_across = 0,
   rope_npos = 0;
@@ -181,8 +186,6 @@ void to_model_input(const Exec& ex, const uint8_t* rgba, int V, int H, int W, fl
 void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count);
 void add_rows(const Exec& ex, float* xs, int rows, int dim, const float* vec);           // xs[r] += vec
 void copy_rows_f32(const Exec& ex, float* dst, long lddst, const float* src, long ldsrc, int rows, int dim);
-// gated[m, j] = silu(x12[m, j]) * x12[m, hidden + j]
-void swiglu_gate(const Exec& ex, int dt, const void* x12, int rows, int hidden, void* out);
 // mean over groups of P rows: out[g, c] = mean_p in[g*P + p, c] (fp32 out)
 void mean_rows(const Exec& ex, int dt, const void* in, int groups, int P, int C, float* out);
 // MA scale head tail + pose quaternion normalisation happen in small kernels:

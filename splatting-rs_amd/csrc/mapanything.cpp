@@ -146,7 +146,7 @@ void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_o
   {
     const size_t m = ar.mark();
     BlockScratch s;
-    block_scratch(ctx_, s, dt_, Te, e, spec_.enc_hidden, spec_.enc_ffn == 1);
+    block_scratch(ctx_, s, dt_, Te, e, spec_.enc_hidden);
     for (int i = 0; i < spec_.enc_depth; ++i) {
       progress(SPLAT_STAGE_BLOCK, i);
       block_forward(ctx_, enc_[i], dt_, xe, xe, Te, V, n, s, 0, n, C, nullptr, 0, i);
@@ -237,7 +237,7 @@ void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_o
   {
     const size_t m = ar.mark();
     BlockScratch s;
-    block_scratch(ctx_, s, dt_, Ti, d, spec_.info_hidden, spec_.info_ffn == 1);
+    block_scratch(ctx_, s, dt_, Ti, d, spec_.info_hidden);
     int stored = 0;
     for (int i = 0; i < spec_.info_depth; ++i) {
       progress(SPLAT_STAGE_BLOCK, spec_.enc_depth + i);

@@ -966,24 +966,6 @@ void copy_rows_f32(const Exec& ex, float* dst, long lddst, const float* src, lon
   SPLAT_HIP(hipGetLastError());
 }
 
-template <typename T>
-__global__ void swiglu_kernel(const void* x12, int rows, int hidden, void* out) {
-  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= (long)rows * hidden) return;
-  const long r = id / hidden, j = id % hidden;
-  const float a = ld<T>(x12, r * 2 * hidden + j), b = ld<T>(x12, r * 2 * hidden + hidden + j);
-  st<T>(out, id, a / (1.f + expf(-a)) * b);
-}
-
-void swiglu_gate(const Exec& ex, int dt, const void* x12, int rows, int hidden, void* out) {
-  if (ex.dry || rows == 0) return;
-  ProfScope ps(ex, "swiglu_gate", 0, 3.0 * rows * hidden * dtype_size(dt));
-  dim3 grid(cdiv((long)rows * hidden, 256));
-  if (dt == F32) hipLaunchKernelGGL(swiglu_kernel<float>, grid, dim3(256), 0, ex.stream, x12, rows, hidden, out);
-  else hipLaunchKernelGGL(swiglu_kernel<bf16>, grid, dim3(256), 0, ex.stream, x12, rows, hidden, out);
-  SPLAT_HIP(hipGetLastError());
-}
-
 // Block (group, 64-column chunk): the 4 waves stride over the P rows, lanes over columns,
 // then the 4 partial sums meet in LDS.
 // Mean over the P rows of each group, in two passes: blocks of (group, 512 channels, slice of

@@ -158,9 +158,21 @@ ConvT Loader::convt(const std::string& name, int cin, int cout, int s) {
   return ct;
 }
 
-Lin Loader::linear_ln(const std::string& name, int n_out, int n_in, const std::string& ln) {
+Lin Loader::linear_ln(const std::string& name, int n_out, int n_in, const std::string& ln, bool glu) {
   auto w = host(name + ".weight", {n_out, n_in});
   auto b = host(name + ".bias", {n_out});
+  if (glu) {  // rows 16j + i: x1 row 8j + i (i < 8), then x2 row hidden + 8j + i - 8
+    const int hidden = n_out / 2;
+    SPLAT_CHECK(n_out % 16 == 0, SHAPE_MISMATCH, name + ": SwiGLU hidden width must be a multiple of 8");
+    std::vector<float> w2(w.size()), b2(b.size());
+    for (int r = 0; r < n_out; ++r) {
+      const int j = r / 16, i = r % 16, src = i < 8 ? 8 * j + i : hidden + 8 * j + i - 8;
+      std::memcpy(&w2[size_t(r) * n_in], &w[size_t(src) * n_in], sizeof(float) * n_in);
+      b2[r] = b[src];
+    }
+    w.swap(w2);
+    b.swap(b2);
+  }
   const auto g = host(ln + ".weight", {n_in});
   const auto beta = host(ln + ".bias", {n_in});
   std::vector<float> c2(n_out);
@@ -207,7 +219,7 @@ Block Loader::block(const std::string& p, int dim, int hidden, bool swiglu, bool
   b.proj = linear(p + ".attn.proj", dim, dim);
   b.ls1 = vec(p + ".ls1.gamma", {dim});
   if (swiglu) {
-    b.fc1 = linear_ln(p + ".mlp.w12", 2 * hidden, dim, p + ".norm2");
+    b.fc1 = linear_ln(p + ".mlp.w12", 2 * hidden, dim, p + ".norm2", true);
     b.fc2 = linear(p + ".mlp.w3", dim, hidden);
   } else {
     b.fc1 = linear_ln(p + ".mlp.fc1", hidden, dim, p + ".norm2");
@@ -219,7 +231,7 @@ Block Loader::block(const std::string& p, int dim, int hidden, bool swiglu, bool
 
 // --- transformer block ----------------------------------------------------------------------
 
-void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, int hidden, bool swiglu) {
+void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, int hidden) {
   const size_t es = dtype_size(dt);
   SPLAT_CHECK(dim % 64 == 0, BAD_ARGUMENT, "transformer width must be a multiple of 64");
   s.h = dt == F32 ? nullptr : ctx.arena.alloc(rows * dim * es);
@@ -230,7 +242,6 @@ void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, in
   s.qkv = ctx.arena.alloc(rows * 3 * dim * es);
   s.att = ctx.arena.alloc(rows * dim * es);
   s.mid = ctx.arena.alloc(rows * hidden * es);
-  s.x12 = swiglu ? ctx.arena.alloc(rows * 2 * hidden * es) : nullptr;
 }
 
 void block_forward(Context& ctx, const Block& b, int dt, const float* in, float* out, long rows, int seqs, int L,
@@ -351,12 +362,12 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
   f1.ldw = b.fc1.ldw;
   f1.bias = b.fc1.b;
   fold(f1, b.fc1);
-  if (b.swiglu) {
+  if (b.swiglu) {  // w3(silu(x1) * x2): the gate in the w12 epilogue (rows interleaved at load)
     f1.N = 2 * b.hidden;
-    f1.out = s.x12;
-    f1.ldc = 2 * b.hidden;
+    f1.glu = 1;
+    f1.out = s.mid;
+    f1.ldc = b.hidden;
     gemm(ex, f1);
-    swiglu_gate(ex, dt, s.x12, int(rows), b.hidden, s.mid);
   } else {
     f1.N = b.hidden;
     f1.act = ACT_GELU;

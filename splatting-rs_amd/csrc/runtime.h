@@ -97,8 +97,9 @@ class Loader {
   std::vector<float> host(const std::string& name, const std::vector<int64_t>& shape);
   Block block(const std::string& name, int dim, int hidden, bool swiglu, bool qk);
   // linear(LN(x)) with the LayerNorm `ln` (weight g, bias beta) folded in: weights w * g
-  // (along K), bias b + w beta, c1 = row sums of the stored (rounded) folded weights.
-  Lin linear_ln(const std::string& name, int n_out, int n_in, const std::string& ln);
+  // (along K), bias b + w beta, c1 = row sums of the stored (rounded) folded weights. glu: a
+  // SwiGLU w12 whose rows are stored interleaved for the fused gate (GemmArgs::glu).
+  Lin linear_ln(const std::string& name, int n_out, int n_in, const std::string& ln, bool glu = false);
   int dt() const { return dt_; }
   // Uploads row-major [n, k] host weights padded to a multiple of 64 columns, as `dt`.
   Lin pack(std::vector<float>& rows, int n, int k, float* bias, int dt);
@@ -134,13 +135,12 @@ struct BlockScratch {
   const float* ln_src = nullptr;
   void* qkv = nullptr;   // [rows, 3*dim]
   void* att = nullptr;   // [rows, dim]
-  void* mid = nullptr;   // [rows, hidden]
-  void* x12 = nullptr;   // [rows, 2*hidden] (SwiGLU only)
+  void* mid = nullptr;   // [rows, hidden] (SwiGLU: the gated product)
 };
 
 class Context;
 
-void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, int hidden, bool swiglu);
+void block_scratch(Context& ctx, BlockScratch& s, int dt, long rows, int dim, int hidden);
 // One pre-norm transformer block over `rows` rows of `in` (fp32 [rows, dim]) into `out`
 // (may equal `in`): sequences of L rows each (`seqs` of them); rope: 0 none, 1 within view,
 // 2 across views (positions from n tokens per view and `cols` patch columns). `block` numbers
