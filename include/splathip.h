@@ -153,6 +153,40 @@ int splat_set_branch_taps(splat_ctx* ctx, splat_branch_tap_fn fn, void* user);
  * Uploads 4 bytes per pixel instead of 12; enqueued on splat_stream. */
 int splat_to_model_input(splat_ctx* ctx, const uint8_t* rgba, int V, int H, int W, float* images, uint8_t* foreground);
 
+/* --- image preprocessing: the crates' load_images from decoded RGBA onwards, on the device ---- */
+
+/* image 0.25.10 imageops::FilterType values the crates resize with (Cargo.lock:2536-2539). */
+enum { SPLAT_FILTER_TRIANGLE = 1, SPLAT_FILTER_CATMULLROM = 2, SPLAT_FILTER_LANCZOS3 = 3 };
+
+/* image::imageops::resize as DynamicImage::resize_exact runs it on an RGBA8 image (called at
+ * depthanything3-rs/src/preprocess.rs:56 and mapanything-rs/src/preprocess.rs:52-56): host RGBA8
+ * [height, width, 4] -> host RGBA8 [new_height, new_width, 4], computed on the device (separable
+ * rows-then-columns passes with the crate's f32 weights, rounded and clamped to u8; a copy at
+ * the same size). */
+int splat_resize_rgba8(splat_ctx* ctx, const uint8_t* src, int width, int height, uint8_t* dst, int new_width,
+                       int new_height, int filter);
+/* depthanything3-rs/src/preprocess.rs:36-45 model_input_size: the longest side to 504, then each
+ * side to the nearest multiple of 14 (no context needed; errors in splat_last_error(NULL)). */
+int splat_da3_input_size(int width, int height, int* bounded_width, int* bounded_height, int* out_width,
+                         int* out_height);
+/* mapanything-rs/src/preprocess.rs:31-41 input_size: the size of the table entry closest to the
+ * mean aspect ratio of n images. */
+int splat_ma_input_size(int n, const int* widths, const int* heights, int* out_width, int* out_height);
+/* depthanything3-rs/src/preprocess.rs:86-123 model_inputs_from_cutouts from the decoded images on:
+ * each host RGBA8 image k [heights[k], widths[k], 4] resized as resize_for_model (to the bounded
+ * size, then to the patch multiples; CatmullRom to enlarge, Triangle to shrink), all center
+ * cropped to the smallest size among them, then to_model_input: device images [n, 3, H, W] f32
+ * ImageNet-normalised and device foreground [n, H, W] u8 (NULL: skipped). images must hold n*3*H*W
+ * floats for the (H, W) that splat_da3_input_size and the minimum over the images give; *out_height
+ * and *out_width receive it. */
+int splat_da3_model_inputs(splat_ctx* ctx, int n, const uint8_t* const* rgba, const int* widths, const int* heights,
+                           float* images, uint8_t* foreground, int* out_height, int* out_width);
+/* mapanything-rs/src/preprocess.rs:66-80 load_images from the decoded images on: every image
+ * resized to cover splat_ma_input_size's (W, H) (Lanczos3 to shrink, CatmullRom to enlarge) and
+ * center cropped to it (cover_and_crop, :43-63), then to_model_input, as splat_da3_model_inputs. */
+int splat_ma_model_inputs(splat_ctx* ctx, int n, const uint8_t* const* rgba, const int* widths, const int* heights,
+                          float* images, uint8_t* foreground, int* out_height, int* out_width);
+
 /* --- Depth Anything 3 ------------------------------------------------------------------------ */
 
 /* weights::load_model(variant, strategy, Some(path), dtype, device), depthanything3-rs/src/weights.rs:26-48

@@ -16,6 +16,21 @@ thread_local std::string g_create_error;
 
 Context* C(splat_ctx* c) { return reinterpret_cast<Context*>(c); }
 
+// Entry points without a context: errors go where splat_last_error(NULL) reads them.
+template <typename F>
+int guard_free(F&& fn) {
+  try {
+    fn();
+    return OK;
+  } catch (const Error& e) {
+    g_create_error = e.what();
+    return e.code;
+  } catch (const std::exception& e) {
+    g_create_error = e.what();
+    return HIP_ERROR;
+  }
+}
+
 template <typename F>
 int guard(Context* ctx, F&& fn) {
   if (!ctx) return BAD_ARGUMENT;
@@ -580,6 +595,63 @@ int splat_to_model_input(splat_ctx* ctx, const uint8_t* rgba, int V, int H, int 
     uint8_t* d = static_cast<uint8_t*>(staging(c, 26, px * 4));
     SPLAT_HIP(hipMemcpyAsync(d, rgba, px * 4, hipMemcpyHostToDevice, c->stream));
     to_model_input(c->ex, d, V, H, W, images, foreground);
+  });
+}
+
+int splat_resize_rgba8(splat_ctx* ctx, const uint8_t* src, int width, int height, uint8_t* dst, int new_width,
+                       int new_height, int filter) {
+  Context* c = C(ctx);
+  return guard(c, [&] {
+    SPLAT_CHECK(src && dst && width > 0 && height > 0 && new_width > 0 && new_height > 0, BAD_ARGUMENT, "resize args");
+    uint8_t* s = static_cast<uint8_t*>(staging(c, 47, size_t(width) * height * 4));
+    uint8_t* d = static_cast<uint8_t*>(staging(c, 48, size_t(new_width) * new_height * 4));
+    SPLAT_HIP(hipMemcpyAsync(s, src, size_t(width) * height * 4, hipMemcpyHostToDevice, c->stream));
+    resize_device(*c, s, width, height, d, new_width, new_height, filter);
+    SPLAT_HIP(hipMemcpyAsync(dst, d, size_t(new_width) * new_height * 4, hipMemcpyDeviceToHost, c->stream));
+    SPLAT_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int splat_da3_input_size(int width, int height, int* bounded_width, int* bounded_height, int* out_width,
+                         int* out_height) {
+  return guard_free([&] {
+    int bw, bh, w, h;
+    da3_model_input_size(width, height, bw, bh, w, h);
+    if (bounded_width) *bounded_width = bw;
+    if (bounded_height) *bounded_height = bh;
+    if (out_width) *out_width = w;
+    if (out_height) *out_height = h;
+  });
+}
+
+int splat_ma_input_size(int n, const int* widths, const int* heights, int* out_width, int* out_height) {
+  return guard_free([&] {
+    int w, h;
+    ma_input_size(n, widths, heights, w, h);
+    if (out_width) *out_width = w;
+    if (out_height) *out_height = h;
+  });
+}
+
+int splat_da3_model_inputs(splat_ctx* ctx, int n, const uint8_t* const* rgba, const int* widths, const int* heights,
+                           float* images, uint8_t* foreground, int* out_height, int* out_width) {
+  Context* c = C(ctx);
+  return guard(c, [&] {
+    int H, W;
+    da3_model_inputs(*c, n, rgba, widths, heights, images, foreground, H, W);
+    if (out_height) *out_height = H;
+    if (out_width) *out_width = W;
+  });
+}
+
+int splat_ma_model_inputs(splat_ctx* ctx, int n, const uint8_t* const* rgba, const int* widths, const int* heights,
+                          float* images, uint8_t* foreground, int* out_height, int* out_width) {
+  Context* c = C(ctx);
+  return guard(c, [&] {
+    int H, W;
+    ma_model_inputs(*c, n, rgba, widths, heights, images, foreground, H, W);
+    if (out_height) *out_height = H;
+    if (out_width) *out_width = W;
   });
 }
 

@@ -182,6 +182,16 @@ void reconstruct_geometry(const Exec& ex, int V, int H, int W, const float* dept
 // RGBA u8 [V,H,W,4] -> normalised images [V,3,H,W] f32 and foreground [V,H,W] (NULL: skipped).
 void to_model_input(const Exec& ex, const uint8_t* rgba, int V, int H, int W, float* img, uint8_t* fg);
 
+// The taps of one resize axis on the device: output coordinate o reads count[o] inputs from
+// first[o], weights w[offset[o] .. offset[o] + count[o]) (normalised, f32).
+struct ResizeTaps {
+  const int* first = nullptr; const int* count = nullptr; const int* offset = nullptr; const float* w = nullptr;
+};
+// RGBA8 [H, W, 4] -> RGBA8 [NH, NW, 4] by image 0.25.10's separable resize: rows (vertical
+// taps, f32 tmp [NH, W, 4]) then columns (horizontal taps, rounded and clamped to u8).
+void resize_rgba8(const Exec& ex, const uint8_t* src, int W, int H, float* tmp, uint8_t* dst, int NW, int NH,
+                  const ResizeTaps& rows, const ResizeTaps& cols);
+
 // Generic elementwise helpers.
 void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count);
 void add_rows(const Exec& ex, float* xs, int rows, int dim, const float* vec);           // xs[r] += vec

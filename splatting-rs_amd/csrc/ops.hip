@@ -1260,4 +1260,69 @@ void to_model_input(const Exec& ex, const uint8_t* rgba, int V, int H, int W, fl
   SPLAT_HIP(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------------------
+// image 0.25.10 imageops::resize on RGBA8 (sample.rs: vertical_sample, then horizontal_sample):
+// pass 1 tmp[y, x] = sum_i w_y[i] * src[first_y + i, x] in f32, taps in order from 0; pass 2
+// dst[y, x] = round_half_away(clamp(sum_i w_x[i] * tmp[y, first_x + i], 0, 255)). Products and
+// sums are rounded separately, as the crate's `t += p * w` (no contraction), so the device
+// reproduces the crate's f32 arithmetic given its weights (computed on the host, preprocess.cpp).
+// One thread per output pixel, 4 channels.
+#pragma clang fp contract(off)
+__global__ void __launch_bounds__(256) resize_rows_kernel(const uint8_t* src, int W, int NH, const int* first,
+                                                          const int* count, const int* offset, const float* wts,
+                                                          float* tmp) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)NH * W) return;
+  const int y = int(id / W), x = int(id - (long)y * W);
+  const int f = first[y], n = count[y];
+  const float* w = wts + offset[y];
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int i = 0; i < n; ++i) {
+    const uchar4 px = reinterpret_cast<const uchar4*>(src)[(long)(f + i) * W + x];
+    const float wi = w[i];
+    a0 = a0 + float(px.x) * wi;
+    a1 = a1 + float(px.y) * wi;
+    a2 = a2 + float(px.z) * wi;
+    a3 = a3 + float(px.w) * wi;
+  }
+  reinterpret_cast<float4*>(tmp)[id] = make_float4(a0, a1, a2, a3);
+}
+
+__device__ inline uint8_t to_u8_nearest(float v) { return uint8_t(roundf(v < 0.f ? 0.f : v > 255.f ? 255.f : v)); }
+
+__global__ void __launch_bounds__(256) resize_cols_kernel(const float* tmp, int W, int NH, int NW, const int* first,
+                                                          const int* count, const int* offset, const float* wts,
+                                                          uint8_t* dst) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)NH * NW) return;
+  const int y = int(id / NW), x = int(id - (long)y * NW);
+  const int f = first[x], n = count[x];
+  const float* w = wts + offset[x];
+  const float4* row = reinterpret_cast<const float4*>(tmp) + (long)y * W + f;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int i = 0; i < n; ++i) {
+    const float4 px = row[i];
+    const float wi = w[i];
+    a0 = a0 + px.x * wi;
+    a1 = a1 + px.y * wi;
+    a2 = a2 + px.z * wi;
+    a3 = a3 + px.w * wi;
+  }
+  reinterpret_cast<uchar4*>(dst)[id] = make_uchar4(to_u8_nearest(a0), to_u8_nearest(a1), to_u8_nearest(a2), to_u8_nearest(a3));
+}
+#pragma clang fp contract(on)
+
+void resize_rgba8(const Exec& ex, const uint8_t* src, int W, int H, float* tmp, uint8_t* dst, int NW, int NH,
+                  const ResizeTaps& rows, const ResizeTaps& cols) {
+  SPLAT_CHECK(W > 0 && H > 0 && NW > 0 && NH > 0, BAD_ARGUMENT, "resize_rgba8 sizes");
+  if (ex.dry) return;
+  ProfScope ps(ex, "resize_rgba8", 0, double(W) * H * 4 + double(NW) * NH * 4);
+  hipLaunchKernelGGL(resize_rows_kernel, dim3(cdiv(long(NH) * W, 256)), dim3(256), 0, ex.stream, src, W, NH, rows.first,
+                     rows.count, rows.offset, rows.w, tmp);
+  SPLAT_HIP(hipGetLastError());
+  hipLaunchKernelGGL(resize_cols_kernel, dim3(cdiv(long(NH) * NW, 256)), dim3(256), 0, ex.stream, tmp, W, NH, NW,
+                     cols.first, cols.count, cols.offset, cols.w, dst);
+  SPLAT_HIP(hipGetLastError());
+}
+
 }  // namespace splat

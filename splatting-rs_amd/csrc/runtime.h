@@ -152,6 +152,27 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
 void block_ln_refresh(Context& ctx, int dt, const float* x, int rows, int dim, BlockScratch& s, int rm_P = 0,
                       int rm_n = 0, int rm_off = 0);
 
+// --- image preprocessing (preprocess.cpp) -----------------------------------------------------
+
+// Host taps of one resize axis (image 0.25.10 sample.rs): output o reads count[o] inputs from
+// first[o] with the normalised weights w[offset[o] ..].
+struct ResizeTapsHost {
+  std::vector<int> first, count, offset;
+  std::vector<float> w;
+};
+ResizeTapsHost resize_taps(int in, int out, int filter);
+void da3_model_input_size(int width, int height, int& bw, int& bh, int& dw, int& dh);
+int da3_resize_filter(int w, int h, int nw, int nh);
+void ma_input_size(int n, const int* widths, const int* heights, int& width, int& height);
+void ma_cover(int w, int h, int width, int height, int& rw, int& rh, int& left, int& top, int& filter);
+// Device RGBA8 [h, w, 4] -> device RGBA8 [nh, nw, 4] (synchronises the context's stream).
+void resize_device(Context& c, const uint8_t* src, int w, int h, uint8_t* dst, int nw, int nh, int filter);
+// The crates' preprocessing of decoded host RGBA8 images into the device model input.
+void da3_model_inputs(Context& c, int n, const uint8_t* const* rgba, const int* widths, const int* heights, float* images,
+                      uint8_t* foreground, int& H, int& W);
+void ma_model_inputs(Context& c, int n, const uint8_t* const* rgba, const int* widths, const int* heights, float* images,
+                     uint8_t* foreground, int& H, int& W);
+
 // GEMM arguments of a convolution on an NHWC map [V, Hi, Wi, cin]: ks == 1 -> plain rows,
 // ks == 3 -> implicit im2col with padding 1. The caller adds epilogue fields.
 GemmArgs conv_args(const Conv& c, int dt, const void* in, int V, int Hi, int Wi, int stride, void* out);

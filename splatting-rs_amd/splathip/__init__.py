@@ -26,6 +26,7 @@ OK, BAD_ARGUMENT, BAD_SHAPE, MISSING_KEY, SHAPE_MISMATCH, HIP_ERROR, NONFINITE, 
 F32, BF16, F16 = 0, 1, 2
 DTYPES = {"f32": F32, "fp32": F32, "bf16": BF16, "f16": F16}
 STAGE_BLOCK, STAGE_DENSE_HEAD, STAGE_CAMERA_HEAD = 0, 1, 2
+FILTER_TRIANGLE, FILTER_CATMULLROM, FILTER_LANCZOS3 = 1, 2, 3   # image 0.25.10 imageops::FilterType
 
 
 class SplatError(RuntimeError):
@@ -121,6 +122,13 @@ SIGNATURES = {
     "splat_kernel_resize_bilinear": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
                                                C.c_void_p, C.c_int, C.c_int]),
     "splat_kernel_reconstruct": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int] + [C.c_void_p] * 11),
+    "splat_resize_rgba8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "splat_da3_input_size": (C.c_int, [C.c_int, C.c_int] + [C.POINTER(C.c_int)] * 4),
+    "splat_ma_input_size": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "splat_da3_model_inputs": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                         C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "splat_ma_model_inputs": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
 }
 
 _lib = None
@@ -305,6 +313,36 @@ class Context:
         self.check(self._lib.splat_to_model_input(self.handle, _ptr(x), V, H, W, C.c_void_p(images_ptr),
                                                   C.c_void_p(foreground_ptr or 0)))
 
+    def resize_rgba8(self, rgba: np.ndarray, new_width: int, new_height: int, filter_type: int) -> np.ndarray:
+        """image::imageops::resize of a host RGBA8 [h, w, 4] image, computed on the device."""
+        x = np.ascontiguousarray(rgba, np.uint8)
+        h, w, _ = x.shape
+        out = np.empty((new_height, new_width, 4), np.uint8)
+        self.check(self._lib.splat_resize_rgba8(self.handle, _ptr(x), w, h, _ptr(out), new_width, new_height,
+                                                filter_type))
+        return out
+
+    def _model_inputs(self, fn, images, images_ptr: int, foreground_ptr: int):
+        xs = [np.ascontiguousarray(im, np.uint8) for im in images]
+        n = len(xs)
+        ptrs = (C.c_void_p * n)(*[x.ctypes.data for x in xs])
+        ws = np.array([x.shape[1] for x in xs], np.int32)
+        hs = np.array([x.shape[0] for x in xs], np.int32)
+        H, W = C.c_int(), C.c_int()
+        self.check(fn(self.handle, n, ptrs, _ptr(ws), _ptr(hs), C.c_void_p(images_ptr), C.c_void_p(foreground_ptr or 0),
+                      C.byref(H), C.byref(W)))
+        return H.value, W.value
+
+    def da3_model_inputs_device(self, images, images_ptr: int, foreground_ptr: int = 0):
+        """depthanything3-rs/src/preprocess.rs:86-123 from decoded host RGBA8 images [h, w, 4] to the
+        device model input (size from da3_model_input_size); returns (H, W)."""
+        return self._model_inputs(self._lib.splat_da3_model_inputs, images, images_ptr, foreground_ptr)
+
+    def ma_model_inputs_device(self, images, images_ptr: int, foreground_ptr: int = 0):
+        """mapanything-rs/src/preprocess.rs:66-80 from decoded host RGBA8 images to the device
+        model input (size from ma_input_size); returns (H, W)."""
+        return self._model_inputs(self._lib.splat_ma_model_inputs, images, images_ptr, foreground_ptr)
+
     def da3_reconstruct(self, images: np.ndarray, foreground=None) -> dict:
         """depthanything3-rs/src/pipeline.rs:52-133 with the geometry on the device."""
         x = np.ascontiguousarray(images, np.float32)
@@ -402,3 +440,30 @@ def reference_ma_spec() -> dict:
     lib().splat_ma_reference_spec(C.byref(s))
     return {name: (list(getattr(s, name)) if name in ("hooks", "dpt_dims") else getattr(s, name))
             for name, _ in MaSpecC._fields_}
+
+
+def _check_free(rc: int):
+    if rc != OK:
+        raise SplatError(rc, lib().splat_last_error(None).decode())
+
+
+def da3_model_input_size(width: int, height: int):
+    """depthanything3-rs/src/preprocess.rs:36-45: ((bounded w, h), (w, h) in patch multiples)."""
+    v = [C.c_int() for _ in range(4)]
+    _check_free(lib().splat_da3_input_size(width, height, *[C.byref(x) for x in v]))
+    return (v[0].value, v[1].value), (v[2].value, v[3].value)
+
+
+def da3_model_inputs_size(sizes):
+    """The common (W, H) of preprocess.rs:86-123 for images of sizes [(w, h)]."""
+    d = [da3_model_input_size(w, h)[1] for w, h in sizes]
+    return min(x[0] for x in d), min(x[1] for x in d)
+
+
+def ma_input_size(sizes):
+    """mapanything-rs/src/preprocess.rs:33-41 for images of sizes [(w, h)]: (W, H)."""
+    ws = np.array([w for w, _ in sizes], np.int32)
+    hs = np.array([h for _, h in sizes], np.int32)
+    W, H = C.c_int(), C.c_int()
+    _check_free(lib().splat_ma_input_size(len(sizes), _ptr(ws), _ptr(hs), C.byref(W), C.byref(H)))
+    return W.value, H.value
