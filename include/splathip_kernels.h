@@ -40,7 +40,9 @@ int splat_kernel_ln_stats(splat_ctx* ctx, const float* x, int rows, int n, int g
                           void* copy);
 
 /* out[s*L + t, h*64 + e] = softmax(q k^T / 8) v for every sequence s < S and head h < heads,
- * reading q, k and v from a [S*L, 3*heads*64] qkv matrix (q | k | v column blocks). */
+ * reading q, k and v from a [S*L, 3*heads*64] qkv matrix (q | k | v column blocks). In bf16
+ * the kernel multiplies q by log2(e)/8 and rounds it to bf16 before the products (the
+ * networks' qkv GEMMs store q already scaled, rounding once). */
 int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads);
 
 /* splat_kernel_attention that allocates nothing. It has no counterpart in the reference; it is

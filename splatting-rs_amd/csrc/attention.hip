@@ -6,9 +6,9 @@
 // accumulator layout (lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32) a
 // lane holds one query (column) and 16 keys per 32-key tile. That same register set is the
 // B operand of O^T = V^T P^T with no data movement: the k-slot order of the P fragment is
-// mirrored when reading V^T, which lives transposed in LDS. Softmax is online (running max
-// and sum per query, base-2 exponent with the 1/8*log2(e) scale folded into one FMA); the
-// row max needs one exchange between lanes l and l^32.
+// mirrored when reading V^T, which lives transposed in LDS. Softmax is online: base-2
+// exponents, the running sum per query, and (generic kernel below) a running max whose row
+// reduction needs one exchange between lanes l and l^32.
 #include "kernels.h"
 
 #include <algorithm>
@@ -300,10 +300,16 @@ __global__ void __launch_bounds__(ATTN_WAVES * 64) attn_kernel(const AttnArgs p,
 // 16-byte chunk). The V^T operand of O^T = V^T P^T is read with ds_read_b64_tr_b16, which
 // transposes 16-bit elements within each group of 16 lanes: no V pass through registers and no
 // VALU transpose (C4 global attention 239 -> 213 us). Rows past the sequence read as zero
-// (buffer range check) and are masked to -inf only in the last tile. The softmax keeps a
-// reference max per query and rescales O and the running sum only when a tile's max exceeds it
-// by more than 2^8 (in exp2 units): O and the sum always share the reference, so the result is
-// exact and P stays below 256.
+// (buffer range check) and are masked to -inf only in the last tile.
+// Softmax: Q comes times log2(e)/8 (from the qkv GEMM's epilogue, or scaled here once per wave),
+// so each score out of the matrix core is already the base-2 exponent s of its weight. The
+// plain pass takes the weights as 2^s against a fixed reference 0: per score one v_exp_f32, a
+// pack to bf16 and half a dot2 for the sum, no row maximum and no rescaling (C4 attention
+// -10%, C5 global -14% against a running maximum). A query whose final sum lies outside
+// [2^-64, 2^64] (logits beyond about +-44, or NaN) sends its block through a second, safe
+// pass that keeps a per-query reference following the running maximum, moved only when a
+// tile's maximum passes it by more than 8: O and the sum always share the reference, so both
+// passes are exact up to rounding.
 
 typedef int int32x4_t __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(3))) char* lds_cptr_a;
@@ -336,7 +342,7 @@ template <int N> __device__ inline void wait_vm() { asm volatile("s_waitcnt vmcn
 }  // namespace
 
 // SPLIT: the block covers key tiles [split * tps, (split + 1) * tps) of its sequence and writes
-// its unnormalised O and (max, sum) to p.part; attn_combine_kernel merges the slices.
+// its unnormalised O and (reference, sum) to p.part; attn_combine_kernel merges the slices.
 template <int WAVES, int QT, bool SPLIT>
 __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(const AttnArgs p, float c) {
   constexpr int KBYTES = 64 * 128;            // K or V tile: 64 keys x 128 bytes, swizzled, unpadded
@@ -368,14 +374,22 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   // nothing: the other waves on its SIMD get the matrix core and the VALU.
   const bool active = __builtin_amdgcn_readfirstlane(q0) < L;
 
+  // Q times c = log2(e)/8, rounded to bf16 once per wave: the products K Q^T are then the
+  // softmax exponents in base 2, with no per-score scaling.
   uint4 qf[QT][4];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qrow = q0 + qt * 32 + l32;
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
-      qf[qt][st] = qrow < L ? *reinterpret_cast<const uint4*>(Q + (base + qrow) * p.ld + st * 16 + g * 8)
-                            : make_uint4(0, 0, 0, 0);
+    for (int st = 0; st < 4; ++st) {
+      const uint4 raw = qrow < L ? *reinterpret_cast<const uint4*>(Q + (base + qrow) * p.ld + st * 16 + g * 8)
+                                 : make_uint4(0, 0, 0, 0);
+      uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = pack_bf16x2(__uint_as_float(w[i] << 16) * c, __uint_as_float(w[i] & 0xffff0000u) * c);
+      qf[qt][st] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
   }
 
   // K and V rows: sequence row s -> byte offset within the buffer that starts at the
@@ -426,16 +440,24 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   // group read, as its element j. So source lane s of group G reads row kA(G) + j (j = (s/4)%4)
   // at head channels dt*32 + 16*(G&1) + 4*(s%4): group G holds d = dt*32 + 16*(G&1) + (0..15)
   // and k-half G>>1.
-  const int G = lane >> 4, vj = (lane >> 2) & 3, vcc = lane & 3;
-  auto vfrag = [&](const char* vt, int kt2, int hh, int dt) {
+  // vbase[dt] is lane l's byte offset for head channels dt*32.. in rows 0..15 of a V tile; the
+  // 16-row groups kt2*32 + 16*hh add constants. It is recomputed in every tile from a copy of
+  // the lane index the compiler cannot hoist: kept across the loop it would be spilled.
+  auto vbases = [&](int (&vbase)[2]) {
+    int ln;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+    const int G = ln >> 4, vj = (ln >> 2) & 3, vcc = ln & 3;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+      vbase[dt] = (4 * (G >> 1) + vj) * 128 + (((4 * dt + 2 * (G & 1) + (vcc >> 1)) ^ (vj << 1)) * 16) + (vcc & 1) * 8;
+  };
+  auto vfrag = [&](const char* vt, const int (&vbase)[2], int kt2, int hh, int dt) {
     typedef short v4s __attribute__((ext_vector_type(4)));
     uint32_t w[4];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int row = kt2 * 32 + 16 * hh + 8 * half + 4 * (G >> 1) + vj;
-      const int chunk = (4 * dt + 2 * (G & 1) + (vcc >> 1)) ^ ((row & 3) << 1);
-      const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) v4s*)((lds_cptr_a)(vt + row * 128 + chunk * 16 + (vcc & 1) * 8)));
+      const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)((
+          lds_cptr_a)(vt + (kt2 * 32 + 16 * hh + 8 * half) * 128 + vbase[dt])));
       const uint2 u = __builtin_bit_cast(uint2, r);
       w[2 * half] = u.x;
       w[2 * half + 1] = u.y;
@@ -445,17 +467,15 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
 
   f32x16 o[QT][2];
   float mref[QT], lsum[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    mref[qt] = -INFINITY;
-    lsum[qt] = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) { o[qt][0][r] = 0.f; o[qt][1][r] = 0.f; }
-  }
   const int sw = (l32 >> 1) & 7;
 
-  auto tile = [&](int t, auto bufc, auto masked_t) {
-    constexpr bool masked = decltype(masked_t)::value;
+  // One 64-key tile. Q arrives times log2(e)/8, so s = K Q^T is the base-2 exponent of each
+  // key's weight. The plain pass (SAFE false) takes the weights as 2^s against a fixed
+  // reference 0: no row maximum and no rescaling. The safe pass keeps a reference per query
+  // that follows the running maximum, moved (and O and the sum rescaled) only when a tile's
+  // maximum passes it by more than 8, so the weights stay below 2^8.
+  auto tile = [&](int t, auto bufc, auto masked_t, auto safe_t) {
+    constexpr bool masked = decltype(masked_t)::value, safe = decltype(safe_t)::value;
     constexpr int B = decltype(bufc)::value;
     const char* kb = smem + B * KBYTES;
     const char* vt = smem + (2 + B) * KBYTES;
@@ -482,52 +502,63 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
           for (int r = 0; r < 16; ++r)
             if (k0 + kt2 * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= L) s[qt][kt2][r] = -INFINITY;
     }
-    bool grow = false;
-    float mnew[QT];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      // 32 scores -> 1 with three-input maxima (v_max3_f32): 10 + 4 + 2 instructions
-      float a[12];
-#pragma unroll
-      for (int i = 0; i < 5; ++i) {
-        a[i] = max3f(s[qt][0][3 * i], s[qt][0][3 * i + 1], s[qt][0][3 * i + 2]);
-        a[5 + i] = max3f(s[qt][1][3 * i], s[qt][1][3 * i + 1], s[qt][1][3 * i + 2]);
-      }
-      a[10] = s[qt][0][15];
-      a[11] = s[qt][1][15];
-      const float b0 = max3f(a[0], a[1], a[2]), b1 = max3f(a[3], a[4], a[5]), b2 = max3f(a[6], a[7], a[8]),
-                  b3 = max3f(a[9], a[10], a[11]);
-      float mx = fmaxf(max3f(b0, b1, b2), b3);
-      // the other half of the query's keys sits in lane l ^ 32: one v_permlane32_swap gives
-      // every lane both halves (a ds_bpermute costs an LDS round trip)
-      const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(sw2[0]), __uint_as_float(sw2[1])) * c;
-      mnew[qt] = mx > mref[qt] + 8.f ? mx : mref[qt];
-      grow |= mnew[qt] != mref[qt];
-    }
-    if (__builtin_amdgcn_ballot_w64(grow)) {
+    if constexpr (safe) {
+      bool grow = false;
+      float mnew[QT];
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
-        const float alpha = __builtin_amdgcn_exp2f(mref[qt] - mnew[qt]);
-        lsum[qt] *= alpha;
+        // 32 exponents -> 1 with three-input maxima (v_max3_f32): 10 + 4 + 2 instructions
+        float a[12];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) { o[qt][0][r] *= alpha; o[qt][1][r] *= alpha; }
-        mref[qt] = mnew[qt];
+        for (int i = 0; i < 5; ++i) {
+          a[i] = max3f(s[qt][0][3 * i], s[qt][0][3 * i + 1], s[qt][0][3 * i + 2]);
+          a[5 + i] = max3f(s[qt][1][3 * i], s[qt][1][3 * i + 1], s[qt][1][3 * i + 2]);
+        }
+        a[10] = s[qt][0][15];
+        a[11] = s[qt][1][15];
+        const float b0 = max3f(a[0], a[1], a[2]), b1 = max3f(a[3], a[4], a[5]), b2 = max3f(a[6], a[7], a[8]),
+                    b3 = max3f(a[9], a[10], a[11]);
+        float mx = fmaxf(max3f(b0, b1, b2), b3);
+        // the other half of the query's keys sits in lane l ^ 32: one v_permlane32_swap gives
+        // every lane both halves (a ds_bpermute costs an LDS round trip)
+        const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mx = fmaxf(__uint_as_float(sw2[0]), __uint_as_float(sw2[1]));
+        mnew[qt] = mx > mref[qt] + 8.f ? mx : mref[qt];
+        grow |= mnew[qt] != mref[qt];
       }
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const float alpha = __builtin_amdgcn_exp2f(mref[qt] - mnew[qt]);
+          lsum[qt] *= alpha;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) { o[qt][0][r] *= alpha; o[qt][1][r] *= alpha; }
+          mref[qt] = mnew[qt];
+        }
+      }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[qt][kt2][r] = __builtin_amdgcn_exp2f(s[qt][kt2][r] - mref[qt]);
+    } else {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[qt][kt2][r] = __builtin_amdgcn_exp2f(s[qt][kt2][r]);
     }
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int kt2 = 0; kt2 < 2; ++kt2)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[qt][kt2][r] = __builtin_amdgcn_exp2f(fmaf(s[qt][kt2][r], c, -mref[qt]));
+    int vbase[2];
+    vbases(vbase);
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
 #pragma unroll
       for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const uint4 vf = vfrag(vt, kt2, hh, dt);
+          const uint4 vf = vfrag(vt, vbase, kt2, hh, dt);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {
             uint4 pf;
@@ -552,33 +583,56 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   const int t0 = SPLIT ? split * p.tps : 0, t1 = SPLIT ? min(ntiles, t0 + p.tps) : ntiles;
   const std::integral_constant<int, 0> R0;
   const std::integral_constant<int, 1> R1;
-  issue(t0, R0);
-  wait_vm<0>();
-  __syncthreads();
-  // Every tile but the last runs without the key mask (a runtime flag inside one loop body was
-  // turned into selects that ran on every tile: ~100 VALU instructions per 64-key tile). Tile t
-  // sits in ring slot (t - t0) & 1; the loop is unrolled by two so that the slot, and with it
-  // every LDS address, is a compile-time constant.
-  auto step = [&](int t, auto bufc) {
-    constexpr int B = decltype(bufc)::value;
-    // slot B ^ 1 held tile t-1, which every wave finished before the last barrier
-    issue(t + 1, std::integral_constant<int, B ^ 1>{});
-    if (active) tile(t, bufc, std::false_type{});
-    wait_vm<0>();  // this wave's share of tile t+1
+  // One pass over the slice's key tiles. Every tile but the last runs without the key mask (a
+  // runtime flag inside one loop body was turned into selects that ran on every tile: ~100
+  // VALU instructions per 64-key tile). Tile t sits in ring slot (t - t0) & 1; the loop is
+  // unrolled by two so that the slot, and with it every LDS address, is a compile-time constant.
+  auto pass = [&](auto safe_t) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      mref[qt] = decltype(safe_t)::value ? -INFINITY : 0.f;
+      lsum[qt] = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { o[qt][0][r] = 0.f; o[qt][1][r] = 0.f; }
+    }
+    issue(t0, R0);
+    wait_vm<0>();
     __syncthreads();
+    auto step = [&](int t, auto bufc) {
+      constexpr int B = decltype(bufc)::value;
+      // slot B ^ 1 held tile t-1, which every wave finished before the last barrier
+      issue(t + 1, std::integral_constant<int, B ^ 1>{});
+      if (active) tile(t, bufc, std::false_type{}, safe_t);
+      wait_vm<0>();  // this wave's share of tile t+1
+      __syncthreads();
+    };
+    int t = t0;
+    for (; t + 2 < t1; t += 2) {
+      step(t, R0);
+      step(t + 1, R1);
+    }
+    if (t + 1 < t1) step(t++, R0);
+    // the slice's last tile, with the key mask (a no-op unless it holds the sequence's ragged
+    // end): one peeled copy, as a second one (unmasked) cost 50 more VGPRs and half the occupancy
+    if (active) {
+      if ((t - t0) & 1) tile(t, R1, std::true_type{}, safe_t);
+      else tile(t, R0, std::true_type{}, safe_t);
+    }
   };
-  int t = t0;
-  for (; t + 2 < t1; t += 2) {
-    step(t, R0);
-    step(t + 1, R1);
+  pass(std::false_type{});
+  // The sum of a query's weights only grows, so a final sum within [2^-64, 2^64] bounds every
+  // weight and partial sum of the plain pass: no overflow, and the largest weight is at least
+  // 2^-64 / L, far above where bf16 or fp32 lose digits. Any other query (logits beyond about
+  // +-44, or NaN) sends its whole block through the safe pass. The last barrier of the pass
+  // also frees the ring for the second one.
+  bool redo = false;
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const auto l2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum[qt]), __float_as_uint(lsum[qt]), false, false);
+    const float tot = __uint_as_float(l2[0]) + __uint_as_float(l2[1]);
+    redo |= active && !(tot >= 0x1p-64f && tot <= 0x1p64f);
   }
-  if (t + 1 < t1) step(t++, R0);
-  // the slice's last tile, with the key mask (a no-op unless it holds the sequence's ragged
-  // end): one peeled copy, as a second one (unmasked) cost 50 more VGPRs and half the occupancy
-  if (active) {
-    if ((t - t0) & 1) tile(t, R1, std::true_type{});
-    else tile(t, R0, std::true_type{});
-  }
+  if (__syncthreads_or(redo)) pass(std::true_type{});
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -618,9 +672,9 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   }
 }
 
-// Merges the key slices of a split launch: per query and head, M = max of the slices' maxima,
-// O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (the maxima are in exp2 units). One thread
-// per 8 head channels.
+// Merges the key slices of a split launch: per query and head, M = max of the slices' exponent
+// references m_s (their maxima, or 0 for a plain pass), O = sum_s 2^(m_s - M) O_s /
+// sum_s 2^(m_s - M) l_s. One thread per 8 head channels.
 template <typename T>
 __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnArgs p) {
   const long rows = long(p.seqs) * p.L;
@@ -702,7 +756,7 @@ void attention(const Exec& ex, const AttnArgs& a) {
   if (ex.dry) return;
   const double rows = double(a.seqs) * a.L * a.heads;
   ProfScope ps(ex, "attention", 4.0 * rows * a.L * 64, 4.0 * rows * 64 * (a.dt == F32 ? 4 : 2));
-  const float c = 0.125f * 1.4426950408889634f;
+  const float c = a.q_scaled ? 1.f : ATTN_Q_SCALE;  // Q times 1 is exact, rounded or not
   if (!bf_fast) {
     const dim3 grid(unsigned(cdiv(a.L, ATTN_WAVES * 32) * b.nsplit), a.heads, a.seqs);
     const long work = long(a.seqs) * a.L * a.heads * 8;

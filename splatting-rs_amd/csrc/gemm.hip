@@ -430,6 +430,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
             }
             qk_norm_rope<RUNS, CH>(p, v, mm, n, lane, wcol0 < 2 * p.qk_dim, xch, xr);
           }
+          if (n < p.q_cols) {
+#pragma unroll
+            for (int t = 0; t < CH; ++t)
+#pragma unroll
+              for (int k = 0; k < 8; ++k) v[t][k] *= p.q_scale;
+          }
         }
         if constexpr (EPI == EPI_LN) {
           if (p.glu) {
@@ -1379,6 +1385,9 @@ void gemm(const Exec& ex, const GemmArgs& args) {
     SPLAT_CHECK(a.ln_in && a.N == 3 * a.qk_dim && a.qk_dim % 64 == 0 && (a.qw == nullptr) == (a.qb == nullptr) &&
                     (a.kw == nullptr) == (a.kb == nullptr) && (!a.rope_cs || (a.rope_n > 0 && a.rope_cols > 0)),
                 BAD_ARGUMENT, "gemm: qk-norm + RoPE need a folded-LayerNorm qkv GEMM");
+  if (a.q_cols)
+    SPLAT_CHECK(a.ln_in && a.q_cols % 8 == 0 && a.q_cols <= a.N && !a.glu, BAD_ARGUMENT,
+                "gemm: the Q scale needs a folded-LayerNorm qkv GEMM");
   if (a.rope_cs && !a.rope_across && a.qk_dim)
     SPLAT_CHECK((a.rope_n - 1) / a.rope_cols + 1 < a.rope_npos && a.rope_cols + 1 <= a.rope_npos, BAD_ARGUMENT,
                 "gemm: RoPE table too small");

@@ -81,6 +81,10 @@ struct GemmArgs {
   int qk_dim = 0; const float* qw = nullptr; const float* qb = nullptr; const float* kw = nullptr;
   const float* kb = nullptr; const float* rope_cs = nullptr; int rope_n = 1, rope_cols = 1, rope_across = 0,
   rope_npos = 0;
+  // Output columns [0, q_cols) times q_scale, last before the store (after the qk-norm and
+  // RoPE; needs a folded-LayerNorm consumer, q_cols a multiple of 8): a qkv GEMM hands the
+  // attention Q already multiplied by its softmax scale (AttnArgs::q_scaled).
+  int q_cols = 0; float q_scale = 1.f;
 };
 // A producer whose tile path cannot emit the statistics (split-K, unaligned, tiles narrower
 // than the group) gets them (and the copy) from ln_stats() on its output.
@@ -103,9 +107,13 @@ struct AttnArgs {
   int L = 0, heads = 0, seqs = 1; long seq_stride = 0;
   // Set by attention() for a key-split launch: nsplit slices of tps 64-key tiles each; part
   // holds the unnormalised fp32 O of every slice, [nsplit][seqs*L][heads*64], then each
-  // slice's (max, sum) per query and head, [nsplit][seqs*L][heads][2].
+  // slice's (exponent reference, sum) per query and head, [nsplit][seqs*L][heads][2].
   int nsplit = 1, tps = 0; float* part = nullptr;
+  // Q already multiplied by log2(e)/8 (ATTN_Q_SCALE) and rounded once; otherwise the bf16
+  // kernel multiplies each Q element by it and rounds it to bf16 again (a second rounding).
+  int q_scaled = 0;
 };
+constexpr float ATTN_Q_SCALE = 0.125f * 1.4426950408889634f;
 void attention(const Exec& ex, const AttnArgs& a);
 
 // Statically allocated device scratch for the key-slice partials of attention launches that

@@ -313,6 +313,10 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
       g.rope_npos = npos;
     }
   }
+  if (dt != F32) {  // Q leaves the epilogue times the softmax scale, rounded to bf16 once
+    g.q_cols = d;
+    g.q_scale = ATTN_Q_SCALE;
+  }
   gemm(ex, g);
   // attention
   AttnArgs a;
@@ -328,6 +332,7 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
   a.heads = b.heads;
   a.seqs = seqs;
   a.seq_stride = L;
+  a.q_scaled = dt != F32;
   attention(ex, a);
   branch_tap(0, b.proj, s.att, d, d);
   // out = in + ls1 * proj(att)

@@ -1,6 +1,8 @@
 """Kernel-level parity of the MFMA GEMM and the flash-attention kernel (through the C ABI's
 kernel entry points, include/splathip_kernels.h) against plain PyTorch fp32/fp64 references
 of the same op on the same bf16/fp32-rounded operands."""
+import math
+
 import numpy as np
 import pytest
 
@@ -138,6 +140,62 @@ def test_attention_matches_torch(ctx, dtype, S, L, heads):
     err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
     report("attention.err", err=f"{err:.2e}")
     assert err < (2e-5 if dtype == "f32" else 2e-2), err
+
+
+# The bf16 kernel's softmax scale: Q times log2(e)/8 in fp32, rounded to bf16 (a second rounding
+# of Q when, as through splat_kernel_attention, Q arrives unscaled), then weights 2^(q'.k).
+Q_SCALE = float(np.float32(0.125) * np.float32(1.4426950408889634))
+
+
+def _attention_ref_scaled(dq, S, L, heads):
+    x = dq.float().reshape(S, L, 3, heads, 64).permute(2, 0, 3, 1, 4)  # [3, S, h, L, 64]
+    q = (x[0] * np.float32(Q_SCALE)).bfloat16().double()
+    p = torch.softmax((q @ x[1].double().transpose(-1, -2)) * math.log(2.0), -1)
+    return (p @ x[2].double()).permute(0, 2, 1, 3).reshape(S * L, heads * 64).cpu()
+
+
+# Logits far outside the usual range, which move the kernel's per-query exponent reference off
+# zero (sums of 2^s beyond 2^64 or below 2^-64): all keys far above, all far below, one key far
+# above the rest in a late tile, and a mix of queries in each regime. Shapes: one and two query
+# sub-tiles per wave, with and without key slices, ragged last tiles. At logits of hundreds the
+# rounding of Q alone moves them by units, so the reference follows the kernel's Q rounding and
+# the test checks the softmax and its reference moves, at the usual tolerance.
+EXTREME_CASES = ["high", "low", "late_peak", "mixed"]
+
+
+@pytest.mark.parametrize("S,L,heads", [(2, 1037, 3), (7, 1037, 16), (1, 6223, 2)])
+@pytest.mark.parametrize("kind", EXTREME_CASES)
+def test_attention_extreme_logits(ctx, kind, S, L, heads):
+    report("attention.extreme", kind=kind, S=S, L=L, heads=heads)
+    g = torch.Generator().manual_seed(L + heads + len(kind))
+    x = torch.randn(S, L, 3, heads, 64, generator=g)
+    u = torch.randn(S, 1, heads, 64, generator=g)
+    u = u / u.norm(dim=-1, keepdim=True)
+    if kind == "high":    # every logit about +600 (natural units), spread of a few units
+        x[:, :, 1] = 8.0 * u + 0.3 * x[:, :, 1]
+        x[:, :, 0] = 600.0 * u + 0.3 * x[:, :, 0]
+    elif kind == "low":   # every logit about -400
+        x[:, :, 1] = 8.0 * u + 0.3 * x[:, :, 1]
+        x[:, :, 0] = -400.0 * u + 0.3 * x[:, :, 0]
+    elif kind == "late_peak":  # ordinary logits, then one key per sequence at +300 in a late tile
+        x[:, :, 0] = 8.0 * u + 0.5 * x[:, :, 0]
+        x[:, L - 40, 1] = 300.0 * u[:, 0]
+    else:                 # queries alternate between the three regimes
+        x[:, :, 1] = 8.0 * u + 0.3 * x[:, :, 1]
+        scale = torch.tensor([600.0, -400.0, 1.0]).repeat(L // 3 + 1)[:L].view(1, L, 1, 1)
+        x[:, :, 0] = scale * u + 0.3 * x[:, :, 0]
+    qkv = x.reshape(S * L, 3 * heads * 64).bfloat16()
+    dq = qkv.cuda()
+    out = torch.empty(S * L, heads * 64, dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+    ctx.kernel_attention(_dt("bf16")[0], dq.data_ptr(), out.data_ptr(), S, L, heads)
+    ctx.synchronize()
+    ref = _attention_ref_scaled(dq, S, L, heads)
+    got = out.cpu().double()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
+    report("attention.extreme.err", err=f"{err:.2e}")
+    assert err < 2e-2, err
 
 
 CONV_CASES = [
