@@ -412,6 +412,40 @@ def test_gemm_folded_layernorm_matches_torch(ctx, dtype, M, N, K, act, group):
     assert err2 < (1e-5 if dtype == "f32" else 2e-2), err2
 
 
+def test_gemm_split_k_repeat(ctx):
+    """Split-K launches (fp32 partials in the context's workspace, summed in slice order by a
+    reduce kernel): each call starts from an output full of NaN, and calls of other shapes in
+    between reuse the same workspace; every call must write every output, bit for bit the first
+    call's result."""
+    outs = {}
+    shapes = [(1297, 384, 1536, "f32"), (100, 256, 4096, "bf16"), (777, 64, 2048, "f32"), (1297, 384, 1536, "f32"),
+              (300, 1001, 2048, "bf16"), (100, 256, 4096, "bf16")]
+    for M, N, K, dtype in shapes:
+        code, tdt = _dt(dtype)
+        g = torch.Generator().manual_seed(M + N + K)
+        A = torch.randn(M, K, generator=g).to(tdt).cuda()
+        ldw = (K + 63) // 64 * 64
+        Wm = torch.zeros(N, ldw)
+        Wm[:, :K] = torch.randn(N, K, generator=g) * 0.05
+        dW = Wm.to(tdt).cuda()
+        b = torch.randn(N, generator=g).cuda()
+        out = torch.full((M, N), float("nan"), dtype=tdt, device="cuda")
+        torch.cuda.synchronize()
+        ctx.kernel_gemm(code, A.data_ptr(), M, K, dW.data_ptr(), N, ldw, b.data_ptr(), 1, out.data_ptr(), False)
+        ctx.synchronize()
+        got = out.cpu()
+        report("gemm.splitk.repeat", M=M, N=N, K=K, dtype=dtype)
+        assert torch.isfinite(got.float()).all()
+        key = (M, N, K, dtype)
+        if key in outs:
+            assert torch.equal(outs[key], got)
+        else:
+            ref = torch.relu(A.cpu().double() @ dW.cpu().double()[:, :K].T + b.cpu().double())
+            err = ((got.double() - ref).abs().max() / ref.abs().max()).item()
+            assert err < (1e-5 if dtype == "f32" else 1e-2), err
+            outs[key] = got
+
+
 LN_PRODUCER_CASES = [
     # (M, N, K, group): proj / fc2 residual epilogues
     (6222, 1024, 1024, 64),   # MapAnything encoder proj: 256x128 tiles
@@ -420,6 +454,7 @@ LN_PRODUCER_CASES = [
     (6223, 768, 3072, 64),    # info fc2
     (5838, 384, 1536, 64),    # DA3-Small C2 fc2: 128x128 tiles
     (1297, 384, 1536, 64),    # DA3-Small C1 fc2: split-K, statistics from the ln_stats kernel
+    (1297, 1536, 1536, 128),  # split-K, 128-column groups
     (1400, 1536, 1536, 128),  # reference-dims MapAnything proj (128-column groups)
     (200, 128, 64, 64),       # one row tile, ragged
 ]
