@@ -106,6 +106,7 @@ template <> struct AttnOps<float> {
 }  // namespace
 
 constexpr int ATTN_WAVES = 4;
+constexpr int ATTN_MAX_SPLITS = 8;  // key slices a launch may use (attn_combine_kernel unrolls over them)
 
 // SPLIT: the block covers key tiles [split * tps, (split + 1) * tps) and writes its unnormalised
 // O and (max, sum) to p.part for attn_combine_kernel, as the bf16 kernel below does.
@@ -684,18 +685,32 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnArgs p) {
   const int rem = int(id - row * p.heads * 8), h = rem >> 3, c8 = (rem & 7) * 8;
   const long so = rows * p.heads * 64;
   const float* ml = p.part + long(p.nsplit) * so;
+  // every slice's loads go out before any is used (one memory latency, not nsplit of them);
+  // the sums run in slice order as before
+  const int ns = p.nsplit;
+  float2 m_l[ATTN_MAX_SPLITS];
+  float4 a[ATTN_MAX_SPLITS], b[ATTN_MAX_SPLITS];
+#pragma unroll
+  for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
+    if (s < ns) {
+      m_l[s] = *reinterpret_cast<const float2*>(ml + ((s * rows + row) * p.heads + h) * 2);
+      const float* src = p.part + s * so + row * p.heads * 64 + h * 64 + c8;
+      a[s] = *reinterpret_cast<const float4*>(src);
+      b[s] = *reinterpret_cast<const float4*>(src + 4);
+    }
   float mx = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s) mx = fmaxf(mx, ml[((s * rows + row) * p.heads + h) * 2]);
+#pragma unroll
+  for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
+    if (s < ns) mx = fmaxf(mx, m_l[s].x);
   float acc[8] = {}, den = 0.f;
-  for (int s = 0; s < p.nsplit; ++s) {
-    const float2 m_l = *reinterpret_cast<const float2*>(ml + ((s * rows + row) * p.heads + h) * 2);
-    const float w = __builtin_amdgcn_exp2f(m_l.x - mx);
-    den += w * m_l.y;
-    const float* src = p.part + s * so + row * p.heads * 64 + h * 64 + c8;
-    const float4 a = *reinterpret_cast<const float4*>(src), b = *reinterpret_cast<const float4*>(src + 4);
-    acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
-    acc[4] += w * b.x; acc[5] += w * b.y; acc[6] += w * b.z; acc[7] += w * b.w;
-  }
+#pragma unroll
+  for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
+    if (s < ns) {
+      const float w = __builtin_amdgcn_exp2f(m_l[s].x - mx);
+      den += w * m_l[s].y;
+      acc[0] += w * a[s].x; acc[1] += w * a[s].y; acc[2] += w * a[s].z; acc[3] += w * a[s].w;
+      acc[4] += w * b[s].x; acc[5] += w * b[s].y; acc[6] += w * b[s].z; acc[7] += w * b[s].w;
+    }
   const float inv = 1.f / den;
   const long seq = row / p.L, t = row - seq * p.L;
   T* dst = reinterpret_cast<T*>(p.o) + (seq * p.seq_stride + t) * p.ldo + h * 64 + c8;
@@ -748,6 +763,7 @@ void attention(const Exec& ex, const AttnArgs& a) {
   if (S > 1) {
     b.tps = cdiv(ntiles, S);
     b.nsplit = cdiv(ntiles, b.tps);  // every slice non-empty
+    SPLAT_CHECK(b.nsplit <= ATTN_MAX_SPLITS, BAD_ARGUMENT, "attention: too many key slices");
     const size_t need = size_t(b.nsplit) * a.seqs * a.L * a.heads * (64 + 2) * sizeof(float);
     if (ex.dry && ex.ws) ex.ws->need = std::max(ex.ws->need, need);
     if (!ex.dry && !(ex.ws && ex.ws->ptr && ex.ws->cap >= need)) b.nsplit = 1;  // not sized: one slice
