@@ -673,6 +673,195 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// fp32 path. 4 waves x 32 queries, 32-key tiles. K and V tiles stream straight into LDS (rows of
+// 256 bytes = 64 fp32 head channels, 16-byte chunk c of tile row r in slot c ^ (r & 15)), two
+// ring slots each. S^T = K Q^T on v_mfma_f32_32x32x2f32: k-step j pairs head channels j and
+// j + 32 (lane half g supplies channel j + 32 g), so a lane reads its key row in 16-byte chunks
+// and holds its query's 32 Q values (times log2(e)/8) in registers. The scores' accumulator
+// layout (lane l, register r: key 8 (r/4) + 4 g + r%4, query l%32) is the B operand of
+// O^T = V^T P^T as it stands: product r takes key 8 (r/4) + 4 g + r%4 in its k-slot g, and the
+// A operand reads that key's V row (head channels dt*32 + l%32) with one ds_read_b32. Softmax:
+// the max-free plain pass and the running-max safe pass of the bf16 kernel, P in fp32.
+template <bool SPLIT>
+__global__ void __launch_bounds__(256, 2) attn_f32_kernel(const AttnArgs p, float c) {
+  constexpr int TB = 32 * 256;  // one 32-key K or V tile
+  __shared__ __attribute__((aligned(1024))) char smem[4 * TB];  // K slots 0, 1 then V slots 0, 1
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, l32 = lane & 31;
+  const int L = p.L;
+  const int nq = (L + 127) / 128;
+  const int ns = SPLIT ? p.nsplit : 1;
+  const int id = xcd_contiguous(blockIdx.x, nq * ns * p.heads * p.seqs);
+  const int qb = id % nq, split = (id / nq) % ns, h = (id / (nq * ns)) % p.heads, sq = id / (nq * ns * p.heads);
+  const long base = long(sq) * p.seq_stride;
+  const int q0 = (qb * 4 + wave) * 32;
+  const bool active = __builtin_amdgcn_readfirstlane(q0) < L;
+
+  float qf[32];  // Q[query q0 + l32][channels 32 g + (0..31)] * c
+  {
+    const int qrow = q0 + l32;
+    const float* Q = reinterpret_cast<const float*>(p.q) + (base + qrow) * p.ld + h * 64 + 32 * g;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 v = qrow < L ? *reinterpret_cast<const float4*>(Q + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qf[4 * i] = v.x * c;
+      qf[4 * i + 1] = v.y * c;
+      qf[4 * i + 2] = v.z * c;
+      qf[4 * i + 3] = v.w * c;
+    }
+  }
+
+  // DMA: load instruction i (0, 1) of wave w fills tile rows 16 i + 4 w + lane/16; lane slot
+  // lane%16 holds chunk (lane%16) ^ (row & 15) of that row.
+  const float* Kseq = reinterpret_cast<const float*>(p.k) + base * p.ld + h * 64;
+  const float* Vseq = reinterpret_cast<const float*>(p.v) + base * p.ld + h * 64;
+  const int32x4_t rk = make_rsrc_a(Kseq, uint32_t(long(L) * p.ld * 4));
+  const int32x4_t rv = make_rsrc_a(Vseq, uint32_t(long(L) * p.ld * 4));
+  int lrw[2];
+  uint32_t goff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    lrw[i] = 16 * i + 4 * wave + (lane >> 4);
+    goff[i] = uint32_t(lrw[i] * p.ld * 4 + (((lane & 15) ^ (lrw[i] & 15)) * 16));
+  }
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>((lds_cptr_a)smem));
+  const uint32_t tile_bytes = uint32_t(32 * p.ld * 4);
+  auto issue = [&](int t, auto bufc) {
+    constexpr int B = decltype(bufc)::value;
+    const uint32_t so = uint32_t(t) * tile_bytes;
+    const bool full = t * 32 + 32 <= L;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t vo = (full || t * 32 + lrw[i] < L) ? goff[i] : 0x80000000u;
+      load_lds_a(rk, vo, so, lds0 + B * TB + (16 * i + 4 * wave) * 256);
+      load_lds_a(rv, vo, so, lds0 + (2 + B) * TB + (16 * i + 4 * wave) * 256);
+    }
+  };
+
+  f32x16 o[2];
+  float mref, lsum;
+  const int ks = l32 & 15;  // row swizzle of this lane's K row (row l32)
+
+  auto tile = [&](int t, auto bufc, auto masked_t, auto safe_t) {
+    constexpr bool masked = decltype(masked_t)::value, safe = decltype(safe_t)::value;
+    constexpr int B = decltype(bufc)::value;
+    const char* kb = smem + B * TB;
+    const char* vb = smem + (2 + B) * TB;
+    f32x16 s = {};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // channels 4 i .. 4 i + 3 (+ 32 g)
+      const float4 kf = *reinterpret_cast<const float4*>(kb + l32 * 256 + (((8 * g + i) ^ ks) * 16));
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[4 * i], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[4 * i + 1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[4 * i + 2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[4 * i + 3], s, 0, 0, 0);
+    }
+    if constexpr (masked) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (t * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= L) s[r] = -INFINITY;
+    }
+    if constexpr (safe) {
+      float mx = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+      const float mnew = mx > mref + 8.f ? mx : mref;
+      if (__builtin_amdgcn_ballot_w64(mnew != mref)) {
+        const float alpha = __builtin_amdgcn_exp2f(mref - mnew);
+        lsum *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { o[0][r] *= alpha; o[1][r] *= alpha; }
+        mref = mnew;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = __builtin_amdgcn_exp2f(s[r] - mref);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = __builtin_amdgcn_exp2f(s[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) lsum += s[r];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int col = dt * 32 + l32;  // head channel of this lane's V reads
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = 8 * (r >> 2) + 4 * g + (r & 3);
+        const float vf = *reinterpret_cast<const float*>(vb + key * 256 + (((col >> 2) ^ (key & 15)) * 16) + (col & 3) * 4);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf, s[r], o[dt], 0, 0, 0);
+      }
+    }
+  };
+
+  const int ntiles = (L + 31) / 32;
+  const int t0 = SPLIT ? split * p.tps : 0, t1 = SPLIT ? min(ntiles, t0 + p.tps) : ntiles;
+  const std::integral_constant<int, 0> R0;
+  const std::integral_constant<int, 1> R1;
+  auto pass = [&](auto safe_t) {
+    mref = decltype(safe_t)::value ? -INFINITY : 0.f;
+    lsum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { o[0][r] = 0.f; o[1][r] = 0.f; }
+    issue(t0, R0);
+    wait_vm<0>();
+    __syncthreads();
+    auto step = [&](int t, auto bufc) {
+      constexpr int B = decltype(bufc)::value;
+      issue(t + 1, std::integral_constant<int, B ^ 1>{});  // slot B ^ 1 held tile t-1, done by all
+      if (active) tile(t, bufc, std::false_type{}, safe_t);
+      wait_vm<0>();
+      __syncthreads();
+    };
+    int t = t0;
+    for (; t + 2 < t1; t += 2) {
+      step(t, R0);
+      step(t + 1, R1);
+    }
+    if (t + 1 < t1) step(t++, R0);
+    if (active) {
+      if ((t - t0) & 1) tile(t, R1, std::true_type{}, safe_t);
+      else tile(t, R0, std::true_type{}, safe_t);
+    }
+  };
+  pass(std::false_type{});
+  const auto l0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum), __float_as_uint(lsum), false, false);
+  float tot = __uint_as_float(l0[0]) + __uint_as_float(l0[1]);
+  if (__syncthreads_or(active && !(tot >= 0x1p-64f && tot <= 0x1p64f))) {
+    pass(std::true_type{});
+    const auto l1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum), __float_as_uint(lsum), false, false);
+    tot = __uint_as_float(l1[0]) + __uint_as_float(l1[1]);
+  }
+
+  const int qrow = q0 + l32;
+  if (qrow >= L) return;
+  if constexpr (SPLIT) {
+    const long row = long(sq) * L + qrow, rows = long(p.seqs) * L;  // dense slice rows
+    float* O = p.part + (long(split) * rows + row) * (long(p.heads) * 64) + h * 64;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(O + dt * 32 + 8 * q4 + 4 * g) =
+            make_float4(o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+    if (g == 0) {
+      float* ml = p.part + long(p.nsplit) * rows * p.heads * 64 + ((long(split) * rows + row) * p.heads + h) * 2;
+      *reinterpret_cast<float2*>(ml) = make_float2(mref, tot);
+    }
+    return;
+  }
+  const float inv = 1.f / tot;
+  float* O = reinterpret_cast<float*>(p.o) + (base + qrow) * p.ldo + h * 64;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+      *reinterpret_cast<float4*>(O + dt * 32 + 8 * q4 + 4 * g) =
+          make_float4(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv, o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+}
+
 // Merges the key slices of a split launch: per query and head, M = max of the slices' exponent
 // references m_s (their maxima, or 0 for a plain pass), O = sum_s 2^(m_s - M) O_s /
 // sum_s 2^(m_s - M) l_s. One thread per 8 head channels.
@@ -744,9 +933,12 @@ void attention(const Exec& ex, const AttnArgs& a) {
   SPLAT_CHECK(a.ld % ke == 0 && a.ldo % 4 == 0 && a.ld >= (long)a.heads * 64, BAD_ARGUMENT, "attention: strides");
   SPLAT_CHECK(a.seqs == 1 || a.seq_stride >= a.L, BAD_ARGUMENT, "attention: overlapping sequences");
   const bool bf_fast = a.dt != F32 && long(a.L) * a.ld * 2 < 2147483648L && a.ld % 8 == 0 && a.ldo % 4 == 0;
-  // fp32 (and the generic bf16 kernel): one block of 128 queries cannot keep a CU busy (fp32
+  auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool f32_fast = a.dt == F32 && long(a.L) * a.ld * 4 < 2147483648L && al16(a.q) && al16(a.k) && al16(a.v) &&
+                        al16(a.o);
+  // fp32 (and the generic kernels): one block of 128 queries cannot keep a CU busy (fp32
   // matrix cores at 1/16 of the bf16 rate), so a small grid is cut into key slices until it
-  // has about two blocks per CU, each slice at least two key tiles (DA3-Small C1: 66 blocks).
+  // has about two blocks per CU (DA3-Small C1: 66 blocks -> 7 slices).
   const long gblocks = long(cdiv(a.L, ATTN_WAVES * 32)) * a.heads * a.seqs;
   // 4 waves x 32 or 64 queries. Two query sub-tiles per wave (QT = 2) halve the K/V reads per
   // query and win once their grid gives each CU about two blocks (C5 global 2.46 vs 2.85 ms);
@@ -756,9 +948,11 @@ void attention(const Exec& ex, const AttnArgs& a) {
   const long blocks2 = long(cdiv(a.L, 256)) * a.heads * a.seqs;
   const bool qt2 = blocks2 >= 500;
   const long blocks = qt2 ? blocks2 : long(cdiv(a.L, 128)) * a.heads * a.seqs;
-  const int ntiles = cdiv(a.L, 64);
-  const int S = bf_fast ? (a.L >= 4096 ? attn_splits(blocks, ntiles) : 1)
-                       : int(std::min<long>(std::min<long>(8, ntiles / 2), std::max<long>(1, cdiv(512, gblocks))));
+  // the fp32 kernel's 32-key tiles: slices of at least 4 tiles, about two blocks per CU
+  const int ntiles = f32_fast ? cdiv(a.L, 32) : cdiv(a.L, 64);
+  const int S = bf_fast    ? (a.L >= 4096 ? attn_splits(blocks, ntiles) : 1)
+                : f32_fast ? int(std::min<long>(std::min<long>(8, std::max(1, ntiles / 4)), std::max<long>(1, cdiv(512, gblocks))))
+                           : int(std::min<long>(std::min<long>(8, ntiles / 2), std::max<long>(1, cdiv(512, gblocks))));
   AttnArgs b = a;
   if (S > 1) {
     b.tps = cdiv(ntiles, S);
@@ -773,7 +967,17 @@ void attention(const Exec& ex, const AttnArgs& a) {
   const double rows = double(a.seqs) * a.L * a.heads;
   ProfScope ps(ex, "attention", 4.0 * rows * a.L * 64, 4.0 * rows * 64 * (a.dt == F32 ? 4 : 2));
   const float c = a.q_scaled ? 1.f : ATTN_Q_SCALE;  // Q times 1 is exact, rounded or not
-  if (!bf_fast) {
+  if (f32_fast) {
+    const dim3 grid(unsigned(long(cdiv(a.L, 128)) * a.heads * a.seqs * b.nsplit));
+    if (b.nsplit > 1) {
+      hipLaunchKernelGGL(attn_f32_kernel<true>, grid, dim3(256), 0, ex.stream, b, c);
+      SPLAT_HIP(hipGetLastError());
+      const long work = long(a.seqs) * a.L * a.heads * 8;
+      hipLaunchKernelGGL(attn_combine_kernel<float>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b);
+    } else {
+      hipLaunchKernelGGL(attn_f32_kernel<false>, grid, dim3(256), 0, ex.stream, b, c);
+    }
+  } else if (!bf_fast) {
     const dim3 grid(unsigned(cdiv(a.L, ATTN_WAVES * 32) * b.nsplit), a.heads, a.seqs);
     const long work = long(a.seqs) * a.L * a.heads * 8;
     const dim3 cgrid(unsigned((work + 255) / 256));
