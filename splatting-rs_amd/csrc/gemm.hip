@@ -7,9 +7,13 @@
 // first 16 bytes of a 32-byte k-step, lanes 32-63 the second; A and W use the same k order,
 // so the sum over k is exact whatever order the hardware walks the fragment in.
 //   bf16: one v_mfma_f32_32x32x16_bf16 per k-step;
-//   fp32: four v_mfma_f32_32x32x2_f32, one per float of the fragment.
-// Accumulator layout (32x32 MFMA): lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4,
-// column l%32.
+//   fp32: 64-byte k-steps on v_mfma_f32_16x16x4_f32 (it sustains ~145 TFLOP/s on this part,
+//   v_mfma_f32_32x32x2_f32 ~120): lane l reads 16 bytes of row l%16 of each 16-row half of a
+//   32-row tile, chunk 4 s + l/16 of the step, and product e of a half pair takes float e of
+//   those fragments (k-slot l/16 = chunk l/16).
+// Accumulator layout per 32x32 tile (f32x16): bf16, lane l, register r -> row 8*(r/4) +
+// 4*(l/32) + r%4, column l%32; fp32, registers 4 (2 mi + ni) + r -> row 16 mi + 4*(l/16) + r,
+// column 16 ni + l%16.
 #include "kernels.h"
 
 #include <algorithm>
@@ -19,6 +23,7 @@ namespace splat {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -39,6 +44,27 @@ template <> struct Mfma<bf16> {
   }
 };
 template <> struct Mfma<float> {
+  // One 64-byte k-step of a 32x32 tile as 2 x 2 halves of 16 rows / 16 columns: a0, a1 the A
+  // fragments of rows 0-15 and 16-31, b0, b1 the W fragments of columns 0-15 and 16-31.
+  __device__ static inline void mma2x2(f32x16& acc, const uint4& a0, const uint4& a1, const uint4& b0,
+                                       const uint4& b1) {
+    f32x4 c0 = acc.s0123, c1 = acc.s4567, c2 = acc.s89ab, c3 = acc.scdef;
+    const float* x0 = reinterpret_cast<const float*>(&a0);
+    const float* x1 = reinterpret_cast<const float*>(&a1);
+    const float* y0 = reinterpret_cast<const float*>(&b0);
+    const float* y1 = reinterpret_cast<const float*>(&b1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(x0[e], y0[e], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(x0[e], y1[e], c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(x1[e], y0[e], c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(x1[e], y1[e], c3, 0, 0, 0);
+    }
+    acc.s0123 = c0;
+    acc.s4567 = c1;
+    acc.s89ab = c2;
+    acc.scdef = c3;
+  }
   __device__ static inline void mma(f32x16& acc, const uint4& a, const uint4& b) {
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
@@ -200,14 +226,23 @@ template <int G> __device__ __forceinline__ float group_sum(float v) {
 constexpr int slab_ld(int tn) { return tn * 32 + 4; }  // +4 floats: conflict-free 16-byte row reads
 
 
-template <int TM, int TN>
+template <int TM, int TN, bool L16>
 __device__ __forceinline__ void stage_slab(const f32x16 (&acc)[TM][TN], int i, float* slab, int lane) {
   constexpr int LD = slab_ld(TN);
-  const int g = lane >> 5, l32 = lane & 31;
+  if constexpr (L16) {  // fp32: 16x16 halves, registers 4 (2 mi + ni) + r
+    const int q = lane >> 4, l16 = lane & 15;
 #pragma unroll
-  for (int j = 0; j < TN; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) slab[(8 * (r >> 2) + 4 * g + (r & 3)) * LD + j * 32 + l32] = acc[i][j][r];
+      for (int r = 0; r < 16; ++r)
+        slab[(16 * (r >> 3) + 4 * q + (r & 3)) * LD + j * 32 + 16 * ((r >> 2) & 1) + l16] = acc[i][j][r];
+  } else {
+    const int g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) slab[(8 * (r >> 2) + 4 * g + (r & 3)) * LD + j * 32 + l32] = acc[i][j][r];
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -315,7 +350,7 @@ __device__ inline void qk_norm_rope(const GemmArgs& p, float (&v)[CH][8], const 
 // `lnab` (EPI_LN): (rstd, -rstd * mean) of this wave's rows in LDS; `xch` (EPI_LN with
 // qk_dim): the block's qk-norm exchange area, xrow0 this wave's first tile row. `lnp`
 // (EPI_RESLN): this wave's corner of the LDS array of 32-column sums, lnp_ld a row.
-template <typename T, int TM, int TN, int EPI>
+template <typename T, int TM, int TN, int EPI, bool L16 = false>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long wrow0, long wcol0, float* slab,
                                          int lane, bool vec, float* part = nullptr, const float* lnab = nullptr,
                                          float* lnp = nullptr, int lnp_ld = 0, float* xch = nullptr, int xrow0 = 0) {
@@ -324,7 +359,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
     // rows of 8 columns: n < N implies n + 8 <= ldp (ldp is N rounded up to 8)
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      stage_slab<TM, TN>(acc, i, slab, lane);
+      stage_slab<TM, TN, L16>(acc, i, slab, lane);
       for (int q = lane; q < 32 * RUNS; q += 64) {
         const int rr = q / RUNS, cc = (q - rr * RUNS) * 8;
         const long m = wrow0 + i * 32 + rr, n = wcol0 + cc;
@@ -339,7 +374,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
   } else if constexpr (EPI == EPI_FULL) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      stage_slab<TM, TN>(acc, i, slab, lane);
+      stage_slab<TM, TN, L16>(acc, i, slab, lane);
       for (int q = lane; q < 32 * RUNS; q += 64) {
         const int rr = q / RUNS, cc = (q - rr * RUNS) * 8;
         const long m = wrow0 + i * 32 + rr, n = wcol0 + cc;
@@ -377,7 +412,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
           lb[t] = ab.y;
         }
       }
-      stage_slab<TM, TN>(acc, i, slab, lane);
+      stage_slab<TM, TN, L16>(acc, i, slab, lane);
 #pragma unroll
       for (int t0 = 0; t0 < IT; t0 += CH) {
         float v[CH][8], rv[CH][8];
@@ -501,7 +536,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
 // lane takes 8 channels of a slab row: h = bf16(relu(acc + bias)), 6 partial dot products with
 // the 1x1 weights, summed over the row's lanes by DPP; the waves' partials per row meet in LDS
 // after the slabs (the ring is free by then), and one thread per pixel finishes the outputs.
-template <typename T, int BM, int BN, int WM, int WN, int TM, int TN>
+template <typename T, int BM, int BN, int WM, int WN, int TM, int TN, bool L16 = false>
 __device__ __forceinline__ void head_epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN], long m0, int wm, int wn,
                                               float* smemf, int wave, int lane, int tid) {
   constexpr int NW = WM * WN, COLS = TN * 32, LD = slab_ld(TN), RUNS = COLS / 8, RPP = 64 / RUNS;
@@ -519,7 +554,7 @@ __device__ __forceinline__ void head_epilogue(const GemmArgs& p, f32x16 (&acc)[T
   for (int k = 0; k < 8; ++k) cb[k] = p.bias[c0 + k];
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    stage_slab<TM, TN>(acc, i, slab, lane);
+    stage_slab<TM, TN, L16>(acc, i, slab, lane);
 #pragma unroll
     for (int t = 0; t < 32 / RPP; ++t) {
       const int rr = rsub + t * RPP;
@@ -778,12 +813,17 @@ template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int AM
 __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32, NW = WM * WN;
   constexpr int ES = sizeof(T), KE = 16 / ES;  // bytes per element, elements per 16-byte chunk
-  constexpr int MPI = ES == 4 ? 4 : 1;         // MFMA instructions per Mfma<T>::mma
+  constexpr int MPI = ES == 4 ? 16 : 1;        // MFMA instructions per tile pair and k-step
   // A tile row holds BK elements = RB bytes = CPR 16-byte chunks; one load instruction of a
   // wave fills RPI rows (1 KiB). Chunk c of row r sits in slot c ^ ((r >> SH) & (CPR - 1)), which
   // keeps the 16 lanes of every ds_read_b128 phase on distinct banks.
-  constexpr int RB = BK * ES, CPR = RB / 16, RPI = 64 / CPR, SH = CPR == 8 ? 1 : 2, KS = RB / 32;
+  constexpr int RB = BK * ES, CPR = RB / 16, RPI = 64 / CPR, SH = CPR == 8 ? 1 : 2;
   static_assert(RB == 128 || RB == 64, "k-tile");
+  // fp32: 64-byte k-steps on 16x16x4 products, two fragments (16-row halves) per 32-row tile
+  constexpr bool L16 = ES == 4;
+  static_assert(!L16 || RB == 128, "fp32 k-tiles are 128 bytes");
+  constexpr int KS = L16 ? RB / 64 : RB / 32;
+  constexpr int FH = L16 ? 2 : 1;  // fragments per 32-row tile per k-step
   constexpr int AL = BM / (NW * RPI), BL = BN / (NW * RPI);  // load instructions per wave per k-tile
   constexpr int LPT = AL + BL;
   static_assert(AL * NW * RPI == BM && BL * NW * RPI == BN, "tile rows split evenly over the waves' loads");
@@ -930,8 +970,12 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int sw = (l32 >> SH) & (CPR - 1);  // fragment rows are l32 plus multiples of 32
-  const int arow0 = (wm * (BM / WM) + l32) * RB, brow0 = (BM + wn * (BN / WN) + l32) * RB;
+  // fragment rows are frow plus multiples of 32 (bf16: l32) or 16 (fp32: l%16)
+  const int frow = L16 ? (lane & 15) : l32, fsub = L16 ? (lane >> 4) : g;
+  const int sw = (frow >> SH) & (CPR - 1);
+  const int arow0 = (wm * (BM / WM) + frow) * RB, brow0 = (BM + wn * (BN / WN) + frow) * RB;
+  // byte offset of this lane's chunk in k-step s of a tile row
+  auto step_off = [&](int st) { return (((L16 ? 4 : 2) * st + fsub) ^ sw) * 16; };
   // Prologue: AHEAD tiles in flight, tile 0 resident for every wave, its first fragments read.
   // Every k-tile slot is loaded, also past the last tile (as zeros), so that the number of
   // loads in flight, and with it each vmcnt wait, is the same for every tile.
@@ -975,23 +1019,32 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   __syncthreads();
   // Fragments of the next k-step (of this tile, or step 0 of the next tile) are read while the
   // matrix cores work on the current one.
-  uint4 fa[2][TM], fb[2][TN];
-  // Fragment f of a k-step in the order the MFMAs (i outer, j inner) first use them: A0, then
-  // every W fragment, then A1..A(TM-1), so that the first MFMAs of a step wait for few reads.
+  uint4 fa[2][TM * FH], fb[2][TN * FH];
+  // Fragment f of a k-step in the order the MFMAs (i outer, j inner) first use them: the A
+  // fragments of tile row 0, then every W fragment, then the other A ones, so that the first
+  // MFMAs of a step wait for few reads. Fragment rows are 32 / FH apart.
   auto read_frag = [&](const char* sb, int off, int slot, int f) {
-    if (f == 0) fa[slot][0] = *reinterpret_cast<const uint4*>(sb + arow0 + off);
-    else if (f <= TN) fb[slot][f - 1] = *reinterpret_cast<const uint4*>(sb + brow0 + (f - 1) * 32 * RB + off);
-    else fa[slot][f - TN] = *reinterpret_cast<const uint4*>(sb + arow0 + (f - TN) * 32 * RB + off);
+    constexpr int RS = 32 / FH * RB;
+    if (f < FH) fa[slot][f] = *reinterpret_cast<const uint4*>(sb + arow0 + f * RS + off);
+    else if (f < FH + TN * FH) fb[slot][f - FH] = *reinterpret_cast<const uint4*>(sb + brow0 + (f - FH) * RS + off);
+    else fa[slot][f - TN * FH] = *reinterpret_cast<const uint4*>(sb + arow0 + (f - TN * FH) * RS + off);
   };
   auto read_frags = [&](const char* sb, int s, int slot) {
-    const int off = ((2 * s + g) ^ sw) * 16;
+    const int off = step_off(s);
 #pragma unroll
-    for (int f = 0; f < TM + TN; ++f) read_frag(sb, off, slot, f);
+    for (int f = 0; f < (TM + TN) * FH; ++f) read_frag(sb, off, slot, f);
+  };
+  // the products of tile pair (i, j) for the k-step whose fragments sit in `slot`
+  auto mma = [&](int i, int j, int slot) {
+    if constexpr (L16)
+      Mfma<float>::mma2x2(acc[i][j], fa[slot][2 * i], fa[slot][2 * i + 1], fb[slot][2 * j], fb[slot][2 * j + 1]);
+    else
+      Mfma<T>::mma(acc[i][j], fa[slot][i], fb[slot][j]);
   };
   read_frags(smem, 0, 0);
   // One k-tile; the last one is peeled (HAS_NEXT false) so that each step's reads and MFMAs
   // share a basic block and the LDS waits stay exact.
-  constexpr int MM = TM * TN, NF = TM + TN, CUR = (KS - 1) & 1;
+  constexpr int MM = TM * TN, NF = (TM + TN) * FH, CUR = (KS - 1) & 1;
   auto tile = [&](int kt, auto has_next, auto full) {
     constexpr bool HAS_NEXT = decltype(has_next)::value;
     const char* sb = smem + (kt % STAGES) * STAGE;
@@ -1001,16 +1054,16 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
       __builtin_amdgcn_sched_barrier(0);
       if (RELU) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa[s & 1][i] = Mfma<T>::relu(fa[s & 1][i]);
+        for (int i = 0; i < TM * FH; ++i) fa[s & 1][i] = Mfma<T>::relu(fa[s & 1][i]);
       }
       if (SPREAD && s + 1 < KS) {
         // this step's share of the loads of tile kt + AHEAD and the reads of the next step's
         // fragments, spread between the MFMAs
         const int L0 = s * LPT / (KS - 1), L1 = (s + 1) * LPT / (KS - 1);
-        const int off = ((2 * (s + 1) + g) ^ sw) * 16;
+        const int off = step_off(s + 1);
 #pragma unroll
         for (int q = 0; q < MM; ++q) {
-          Mfma<T>::mma(acc[q / TN][q % TN], fa[s & 1][q / TN], fb[s & 1][q % TN]);
+          mma(q / TN, q % TN, s & 1);
 #pragma unroll
           for (int l = L0 + q * (L1 - L0) / MM; l < L0 + (q + 1) * (L1 - L0) / MM; ++l)
             issue_one(kt + AHEAD, (kt + AHEAD) % STAGES, l, full);
@@ -1023,7 +1076,7 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j) Mfma<T>::mma(acc[i][j], fa[s & 1][i], fb[s & 1][j]);
+          for (int j = 0; j < TN; ++j) mma(i, j, s & 1);
         if (s + 1 < KS) {
           // interleave the LDS reads with this step's MFMAs
 #pragma unroll
@@ -1041,10 +1094,10 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
         wait_vmcnt<(STAGES - 2) * LPT>();
         __syncthreads();
         const char* nb = smem + ((kt + 1) % STAGES) * STAGE;
-        const int off0 = (g ^ sw) * 16;
+        const int off0 = step_off(0);
 #pragma unroll
         for (int q = 0; q < MM; ++q) {
-          Mfma<T>::mma(acc[q / TN][q % TN], fa[CUR][q / TN], fb[CUR][q % TN]);
+          mma(q / TN, q % TN, CUR);
           if constexpr (!SPREAD) {
 #pragma unroll
             for (int l = q * LPT / MM; l < (q + 1) * LPT / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l, full);
@@ -1066,12 +1119,12 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
   if constexpr (EPI == EPI_HEAD) {
     static_assert(NW * 32 * slab_ld(TN) * 4 + BM * WN * 6 * 4 <= STAGES * STAGE, "head epilogue LDS");
-    head_epilogue<T, BM, BN, WM, WN, TM, TN>(p, acc, m0, wm, wn, reinterpret_cast<float*>(smem), wave, lane, tid);
+    head_epilogue<T, BM, BN, WM, WN, TM, TN, L16>(p, acc, m0, wm, wn, reinterpret_cast<float*>(smem), wave, lane, tid);
   } else {
     float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
     constexpr int LNLD = BN / 32;  // 32-column sums per tile row (EPI_RESLN)
     float* lnp = reinterpret_cast<float*>(smem) + NW * 32 * slab_ld(TN);
-    epilogue<T, TM, TN, EPI>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
+    epilogue<T, TM, TN, EPI, L16>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
                              EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr, lnab + wm * (BM / WM) * 2,
                              lnp + (wm * (BM / WM) * LNLD + wn * (BN / WN) / 32) * 2, LNLD,
                              lnp + (wn / 2) * BM * 4, wm * (BM / WM));
