@@ -10,6 +10,7 @@ bf16. Prints one JSON line; details go to stderr.
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C1..C5]
 """
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -21,7 +22,7 @@ for p in (ROOT, os.path.join(ROOT, "splatting-rs_amd")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
-PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}   # dense MFMA, MI355X
+PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}   # dense MFMA, MI355X
 PEAK_HBM_GBS = 8000.0
 MFMA_KERNELS = ("gemm", "conv_igemm", "attention")
 COPY_CAL_BYTES = 256 << 20
@@ -219,6 +220,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="C4", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--dtype", choices=["bf16", "f16", "f32"], default=None,
+                    help="model dtype (default: the configuration's, bf16 for the benchmark line)")
     ap.add_argument("--no-graphs", action="store_true", help="eager launches instead of HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
@@ -248,6 +251,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     cfg = specs.CONFIGS[args.config]
+    if args.dtype and args.dtype != cfg.dtype:
+        cfg = dataclasses.replace(cfg, dtype=args.dtype,
+                                  description=cfg.description.replace(f", {cfg.dtype}", f", {args.dtype}"))
     host = host_cpu()
     ctx = splathip.Context(0)
     with tempfile.TemporaryDirectory(dir="/tmp") as tmp:

@@ -46,9 +46,9 @@ typedef enum splat_status {
 } splat_status;
 
 /* The model dtype of the loaders (candle's DType, depthanything3-rs/src/main.rs:60-61,
- * mapanything-rs/src/main.rs:59-60). SPLAT_F16 is declared for the reference's --precision f16
- * but not implemented: the loaders return SPLAT_BAD_ARGUMENT for it rather than computing in
- * another precision than the one asked for. */
+ * mapanything-rs/src/main.rs:59-60): the storage type of the weights and of the activations the
+ * matrix cores read (SPLAT_BF16 and SPLAT_F16 on the 16-bit MFMA instructions, fp32 accumulation;
+ * the residual stream stays fp32 in every dtype). */
 typedef enum splat_dtype { SPLAT_F32 = 0, SPLAT_BF16 = 1, SPLAT_F16 = 2 } splat_dtype;
 
 /* depthanything3-rs/src/variant.rs:17-23 */

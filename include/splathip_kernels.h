@@ -12,7 +12,10 @@
 extern "C" {
 #endif
 
-/* C[M, N] = act(A[M, K] W[N, K]^T + bias) ; A, W in `dtype` (SPLAT_F32 / SPLAT_BF16), W with
+/* `dtype` of every entry point below: SPLAT_F32, SPLAT_BF16 or SPLAT_F16 (the storage type of
+ * the 16-bit or fp32 operands named as "in `dtype`"); accumulation is fp32 in all three.
+ *
+ * C[M, N] = act(A[M, K] W[N, K]^T + bias) ; A, W in `dtype`, W with
  * row stride ldw (a multiple of 64, columns K..ldw-1 zero), C fp32 when out_f32 else `dtype`.
  * act: 0 none, 1 relu, 2 gelu (erf). */
 int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, const void* W, int N, int ldw,
@@ -41,8 +44,9 @@ int splat_kernel_ln_stats(splat_ctx* ctx, const float* x, int rows, int n, int g
 
 /* out[s*L + t, h*64 + e] = softmax(q k^T / 8) v for every sequence s < S and head h < heads,
  * reading q, k and v from a [S*L, 3*heads*64] qkv matrix (q | k | v column blocks). In bf16
- * the kernel multiplies q by log2(e)/8 and rounds it to bf16 before the products (the
- * networks' qkv GEMMs store q already scaled, rounding once). */
+ * and f16 the kernel multiplies q by log2(e)/8 and rounds it to that type before the products
+ * (the networks' qkv GEMMs store q already scaled, rounding once); the weights P go to the
+ * matrix cores rounded to the same type. */
 int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads);
 
 /* splat_kernel_attention that allocates nothing. It has no counterpart in the reference; it is

@@ -51,8 +51,29 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// 32x32x16 product of 16-bit operand fragments (8 values a lane) of storage type H
+template <typename H> __device__ inline f32x16 mma16(const uint4& a, const uint4& b, const f32x16& c);
+template <> __device__ inline f32x16 mma16<bf16>(const uint4& a, const uint4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+template <> __device__ inline f32x16 mma16<f16>(const uint4& a, const uint4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+// acc + the two values of a packed pair (one v_dot2 against a pair of ones)
+template <typename H> __device__ inline float add_pair(uint32_t pair, float acc);
+template <> __device__ inline float add_pair<bf16>(uint32_t pair, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), __builtin_bit_cast(bf16x2_t, 0x3f803f80u), acc,
+                                         false);
+}
+template <> __device__ inline float add_pair<f16>(uint32_t pair, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
+}
+
 template <typename T> struct AttnOps;
-template <> struct AttnOps<bf16> {
+template <typename H> struct AttnOps16 {
   // O^T[d][q] += V^T[d][keys] P^T[keys][q] for the 32 keys of sub-tile kt2.
   __device__ static inline void pv(f32x16& o, const char* vrow, int kt2, int g, const f32x16& s) {
 #pragma unroll
@@ -65,22 +86,20 @@ template <> struct AttnOps<bf16> {
       uint32_t* pw = reinterpret_cast<uint32_t*>(&pf);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        pw[i] = pack_bf16x2(s[8 * hh + 2 * i], s[8 * hh + 2 * i + 1]);
-      o = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf), __builtin_bit_cast(bf16x8_t, pf),
-                                                  o, 0, 0, 0);
+        pw[i] = pack2<H>(s[8 * hh + 2 * i], s[8 * hh + 2 * i + 1]);
+      o = mma16<H>(vf, pf, o);
     }
   }
-  __device__ static inline void qk(f32x16& acc, const uint4& kf, const uint4& qf) {
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf), __builtin_bit_cast(bf16x8_t, qf),
-                                                  acc, 0, 0, 0);
-  }
+  __device__ static inline void qk(f32x16& acc, const uint4& kf, const uint4& qf) { acc = mma16<H>(kf, qf, acc); }
   __device__ static inline void store4(void* dst, const float* v) {
     uint2 w;
-    w.x = pack_bf16x2(v[0], v[1]);
-    w.y = pack_bf16x2(v[2], v[3]);
+    w.x = pack2<H>(v[0], v[1]);
+    w.y = pack2<H>(v[2], v[3]);
     *reinterpret_cast<uint2*>(dst) = w;
   }
 };
+template <> struct AttnOps<bf16> : AttnOps16<bf16> {};
+template <> struct AttnOps<f16> : AttnOps16<f16> {};
 template <> struct AttnOps<float> {
   __device__ static inline void pv(f32x16& o, const char* vrow, int kt2, int g, const f32x16& s) {
 #pragma unroll
@@ -344,7 +363,8 @@ template <int N> __device__ inline void wait_vm() { asm volatile("s_waitcnt vmcn
 
 // SPLIT: the block covers key tiles [split * tps, (split + 1) * tps) of its sequence and writes
 // its unnormalised O and (reference, sum) to p.part; attn_combine_kernel merges the slices.
-template <int WAVES, int QT, bool SPLIT>
+// H: the 16-bit storage type of Q, K, V and O (bf16 or f16).
+template <int WAVES, int QT, bool SPLIT, typename H = bf16>
 __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(const AttnArgs p, float c) {
   constexpr int KBYTES = 64 * 128;            // K or V tile: 64 keys x 128 bytes, swizzled, unpadded
   constexpr int KL = 8 / WAVES;               // load instructions per wave per K (or V) tile
@@ -375,7 +395,7 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   // nothing: the other waves on its SIMD get the matrix core and the VALU.
   const bool active = __builtin_amdgcn_readfirstlane(q0) < L;
 
-  // Q times c = log2(e)/8, rounded to bf16 once per wave: the products K Q^T are then the
+  // Q times c = log2(e)/8, rounded to H once per wave: the products K Q^T are then the
   // softmax exponents in base 2, with no per-score scaling.
   uint4 qf[QT][4];
 #pragma unroll
@@ -388,7 +408,7 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
       uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        w[i] = pack_bf16x2(__uint_as_float(w[i] << 16) * c, __uint_as_float(w[i] & 0xffff0000u) * c);
+        w[i] = pack2<H>(u16f<H>(w[i]) * c, u16f<H>(w[i] >> 16) * c);
       qf[qt][st] = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
@@ -489,9 +509,7 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
         const uint4 kf = *reinterpret_cast<const uint4*>(kb + (kt2 * 32 + l32) * 128 + ((2 * st + g) ^ sw) * 16);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)  // the first k-step starts from a zero accumulator operand
-          s[qt][kt2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
-                                                               __builtin_bit_cast(bf16x8_t, qf[qt][st]),
-                                                               st == 0 ? zero : s[qt][kt2], 0, 0, 0);
+          s[qt][kt2] = mma16<H>(kf, qf[qt][st], st == 0 ? zero : s[qt][kt2]);
       }
     if constexpr (masked) {  // the peeled last tile only
       const int k0 = t * 64;
@@ -566,14 +584,11 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
             uint32_t* pw = reinterpret_cast<uint32_t*>(&pf);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              pw[i] = pack_bf16x2(s[qt][kt2][8 * hh + 2 * i], s[qt][kt2][8 * hh + 2 * i + 1]);
-            o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf),
-                                                                __builtin_bit_cast(bf16x8_t, pf), o[qt][dt], 0, 0, 0);
-            if (dt == 0) {  // the running sum of the bf16 P the matrix cores use: one dot2 per pair
+              pw[i] = pack2<H>(s[qt][kt2][8 * hh + 2 * i], s[qt][kt2][8 * hh + 2 * i + 1]);
+            o[qt][dt] = mma16<H>(vf, pf, o[qt][dt]);
+            if (dt == 0) {  // the running sum of the rounded P the matrix cores use: one dot2 per pair
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                lsum[qt] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw[i]),
-                                                           __builtin_bit_cast(bf16x2_t, 0x3f803f80u), lsum[qt], false);
+              for (int i = 0; i < 4; ++i) lsum[qt] = add_pair<H>(pw[i], lsum[qt]);
             }
           }
         }
@@ -621,17 +636,21 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
     }
   };
   pass(std::false_type{});
-  // The sum of a query's weights only grows, so a final sum within [2^-64, 2^64] bounds every
-  // weight and partial sum of the plain pass: no overflow, and the largest weight is at least
-  // 2^-64 / L, far above where bf16 or fp32 lose digits. Any other query (logits beyond about
-  // +-44, or NaN) sends its whole block through the safe pass. The last barrier of the pass
-  // also frees the ring for the second one.
+  // The sum of a query's weights only grows, so a final sum within [lo, hi] bounds every weight
+  // and partial sum of the plain pass. bf16: [2^-64, 2^64]; no overflow, and the largest weight is
+  // at least 2^-64 / L, far above where bf16 or fp32 lose digits. f16 (largest value 65504,
+  // subnormal below 2^-14): [L 2^-12, 2^15]; every weight stays below 65504, and the weights
+  // that land among the subnormals (rounding error at most 2^-25 each) move the sum by less than
+  // 2^-13 of itself. Any other query (large logits, or NaN) sends its whole block through the
+  // safe pass. The last barrier of the pass also frees the ring for the second one.
+  constexpr bool half = std::is_same_v<H, f16>;
+  const float lo = half ? float(L) * 0x1p-12f : 0x1p-64f, hi = half ? 0x1p15f : 0x1p64f;
   bool redo = false;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const auto l2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum[qt]), __float_as_uint(lsum[qt]), false, false);
     const float tot = __uint_as_float(l2[0]) + __uint_as_float(l2[1]);
-    redo |= active && !(tot >= 0x1p-64f && tot <= 0x1p64f);
+    redo |= active && !(tot >= lo && tot <= hi);
   }
   if (__syncthreads_or(redo)) pass(std::true_type{});
 
@@ -667,7 +686,7 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = o[qt][dt][4 * q4 + e] * inv;
-          AttnOps<bf16>::store4(O + dt * 32 + 8 * q4 + 4 * g, v);
+          AttnOps<H>::store4(O + dt * 32 + 8 * q4 + 4 * g, v);
         }
     }
   }
@@ -927,6 +946,36 @@ static int attn_splits(long blocks, int ntiles) {
   return best;
 }
 
+// The launches of a 16-bit (bf16 or f16) attention: the fast kernel, or the generic one for
+// strides it does not take; then the slice merge when b is split.
+template <typename H>
+static void launch16(const Exec& ex, const AttnArgs& b, float c, bool fast, bool qt2, long blocks) {
+  const long work = long(b.seqs) * b.L * b.heads * 8;
+  const dim3 cgrid(unsigned((work + 255) / 256));
+  if (!fast) {
+    const dim3 grid(unsigned(cdiv(b.L, ATTN_WAVES * 32) * b.nsplit), b.heads, b.seqs);
+    if (b.nsplit > 1) {
+      hipLaunchKernelGGL((attn_kernel<H, true>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
+      SPLAT_HIP(hipGetLastError());
+      hipLaunchKernelGGL(attn_combine_kernel<H>, cgrid, dim3(256), 0, ex.stream, b);
+    } else {
+      hipLaunchKernelGGL((attn_kernel<H, false>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
+    }
+    return;
+  }
+  const dim3 grid(unsigned(blocks * b.nsplit));
+  if (b.nsplit > 1) {
+    if (qt2) hipLaunchKernelGGL((attn_bf16_kernel<4, 2, true, H>), grid, dim3(256), 0, ex.stream, b, c);
+    else hipLaunchKernelGGL((attn_bf16_kernel<4, 1, true, H>), grid, dim3(256), 0, ex.stream, b, c);
+    SPLAT_HIP(hipGetLastError());
+    hipLaunchKernelGGL(attn_combine_kernel<H>, cgrid, dim3(256), 0, ex.stream, b);
+  } else if (qt2) {
+    hipLaunchKernelGGL((attn_bf16_kernel<4, 2, false, H>), grid, dim3(256), 0, ex.stream, b, c);
+  } else {
+    hipLaunchKernelGGL((attn_bf16_kernel<4, 1, false, H>), grid, dim3(256), 0, ex.stream, b, c);
+  }
+}
+
 void attention(const Exec& ex, const AttnArgs& a) {
   const int ke = a.dt == F32 ? 4 : 8;
   SPLAT_CHECK(a.L > 0 && a.heads > 0 && a.seqs > 0, BAD_ARGUMENT, "attention: bad sizes");
@@ -977,40 +1026,20 @@ void attention(const Exec& ex, const AttnArgs& a) {
     } else {
       hipLaunchKernelGGL(attn_f32_kernel<false>, grid, dim3(256), 0, ex.stream, b, c);
     }
-  } else if (!bf_fast) {
+  } else if (a.dt == F32) {
     const dim3 grid(unsigned(cdiv(a.L, ATTN_WAVES * 32) * b.nsplit), a.heads, a.seqs);
-    const long work = long(a.seqs) * a.L * a.heads * 8;
-    const dim3 cgrid(unsigned((work + 255) / 256));
-    if (a.dt == F32) {
-      if (b.nsplit > 1) {
-        hipLaunchKernelGGL((attn_kernel<float, true>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
-        SPLAT_HIP(hipGetLastError());
-        hipLaunchKernelGGL(attn_combine_kernel<float>, cgrid, dim3(256), 0, ex.stream, b);
-      } else {
-        hipLaunchKernelGGL((attn_kernel<float, false>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
-      }
-    } else {
-      if (b.nsplit > 1) {
-        hipLaunchKernelGGL((attn_kernel<bf16, true>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
-        SPLAT_HIP(hipGetLastError());
-        hipLaunchKernelGGL(attn_combine_kernel<bf16>, cgrid, dim3(256), 0, ex.stream, b);
-      } else {
-        hipLaunchKernelGGL((attn_kernel<bf16, false>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
-      }
-    }
-  } else {
-    const dim3 grid(unsigned(blocks * b.nsplit));
     if (b.nsplit > 1) {
-      if (qt2) hipLaunchKernelGGL((attn_bf16_kernel<4, 2, true>), grid, dim3(256), 0, ex.stream, b, c);
-      else hipLaunchKernelGGL((attn_bf16_kernel<4, 1, true>), grid, dim3(256), 0, ex.stream, b, c);
+      hipLaunchKernelGGL((attn_kernel<float, true>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
       SPLAT_HIP(hipGetLastError());
       const long work = long(a.seqs) * a.L * a.heads * 8;
-      hipLaunchKernelGGL(attn_combine_kernel<bf16>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b);
-    } else if (qt2) {
-      hipLaunchKernelGGL((attn_bf16_kernel<4, 2, false>), grid, dim3(256), 0, ex.stream, b, c);
+      hipLaunchKernelGGL(attn_combine_kernel<float>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b);
     } else {
-      hipLaunchKernelGGL((attn_bf16_kernel<4, 1, false>), grid, dim3(256), 0, ex.stream, b, c);
+      hipLaunchKernelGGL((attn_kernel<float, false>), grid, dim3(ATTN_WAVES * 64), 0, ex.stream, b, c);
     }
+  } else if (a.dt == F16) {
+    launch16<f16>(ex, b, c, bf_fast, qt2, blocks);
+  } else {
+    launch16<bf16>(ex, b, c, bf_fast, qt2, blocks);
   }
   SPLAT_HIP(hipGetLastError());
 }

@@ -51,11 +51,10 @@ int guard(Context* ctx, F&& fn) {
   }
 }
 
+// splat_dtype -> the library's storage type (the values agree; unknown values are rejected)
 int model_dtype(int dtype) {
-  SPLAT_CHECK(dtype != SPLAT_F16, BAD_ARGUMENT,
-              "dtype SPLAT_F16 is not implemented (use SPLAT_BF16 or SPLAT_F32; no silent narrowing to bf16)");
-  SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "unknown dtype");
-  return dtype == SPLAT_F32 ? F32 : BF16;
+  SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16 || dtype == SPLAT_F16, BAD_ARGUMENT, "unknown dtype");
+  return dtype == SPLAT_F32 ? F32 : dtype == SPLAT_F16 ? F16 : BF16;
 }
 
 void check_images(const float* images, int V, int H, int W) {
@@ -134,9 +133,8 @@ void load_da3(Context* ctx, SafeTensors& st, int variant, int dtype, int strateg
 }
 
 AttnArgs attention_args(int dtype, const void* qkv, void* out, int S, int L, int heads) {
-  SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
   AttnArgs a;
-  a.dt = dtype == SPLAT_F32 ? F32 : BF16;
+  a.dt = model_dtype(dtype);
   const size_t es = dtype_size(a.dt);
   a.q = qkv;
   a.k = static_cast<const char*>(qkv) + size_t(heads) * 64 * es;
@@ -368,10 +366,9 @@ static void gemm_now(Context* c, const GemmArgs& g) {
 int splat_kernel_gemm(splat_ctx* ctx, int dtype, const void* A, int M, int K, const void* W, int N, int ldw,
                       const float* bias, int act, void* out, int out_f32) {
   return guard(C(ctx), [&] {
-    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
     SPLAT_CHECK(act >= 0 && act <= 2, BAD_ARGUMENT, "act");
     GemmArgs g;
-    g.dt = dtype == SPLAT_F32 ? F32 : BF16;
+    g.dt = model_dtype(dtype);
     g.M = M;
     g.N = N;
     g.K = K;
@@ -393,7 +390,6 @@ int splat_kernel_gemm_ln(splat_ctx* ctx, int dtype, const void* A, int M, int K,
                          const float* gamma, const float* res, float* ln_out, void* copy, int group, void* out,
                          int out_f32) {
   return guard(C(ctx), [&] {
-    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
     SPLAT_CHECK(act >= 0 && act <= 2, BAD_ARGUMENT, "act");
     SPLAT_CHECK(group == 64 || group == 128, BAD_ARGUMENT, "statistics group: 64 or 128 columns");
     SPLAT_CHECK(!ln_in || K % group == 0, BAD_ARGUMENT, "folded LayerNorm: K must be a multiple of the group");
@@ -401,7 +397,7 @@ int splat_kernel_gemm_ln(splat_ctx* ctx, int dtype, const void* A, int M, int K,
     SPLAT_CHECK(!res || out_f32, BAD_ARGUMENT, "residual epilogue: fp32 output");
     SPLAT_CHECK(!ln_out || res, BAD_ARGUMENT, "row statistics come from the residual epilogue");
     GemmArgs g;
-    g.dt = dtype == SPLAT_F32 ? F32 : BF16;
+    g.dt = model_dtype(dtype);
     g.M = M;
     g.N = N;
     g.K = K;
@@ -436,8 +432,7 @@ int splat_kernel_gemm_ln(splat_ctx* ctx, int dtype, const void* A, int M, int K,
 int splat_kernel_ln_stats(splat_ctx* ctx, const float* x, int rows, int n, int group, float* stats, int dtype,
                           void* copy) {
   return guard(C(ctx), [&] {
-    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
-    ln_stats(C(ctx)->ex, x, n, rows, n, group, stats, dtype == SPLAT_F32 ? F32 : BF16, copy);
+    ln_stats(C(ctx)->ex, x, n, rows, n, group, stats, model_dtype(dtype), copy);
   });
 }
 
@@ -521,7 +516,6 @@ int splat_kernel_conv2d(splat_ctx* ctx, int dtype, const void* in, int V, int H,
                         int Cout, int ldw, int ks, int stride, const float* bias, int relu_in, int act,
                         const void* res, void* out) {
   return guard(C(ctx), [&] {
-    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
     SPLAT_CHECK(ks == 1 || ks == 3, BAD_ARGUMENT, "kernel size must be 1 or 3");
     Conv c;
     c.cout = Cout;
@@ -532,7 +526,7 @@ int splat_kernel_conv2d(splat_ctx* ctx, int dtype, const void* in, int V, int H,
     c.lin.N = Cout;
     c.lin.K = ks * ks * Cin;
     c.lin.b = const_cast<float*>(bias);
-    const int dt = dtype == SPLAT_F32 ? F32 : BF16;
+    const int dt = model_dtype(dtype);
     GemmArgs g = conv_args(c, dt, in, V, H, W, stride, out);
     g.relu_in = relu_in;
     g.act = act;
@@ -545,14 +539,13 @@ int splat_kernel_conv2d(splat_ctx* ctx, int dtype, const void* in, int V, int H,
 int splat_kernel_conv_transpose2d(splat_ctx* ctx, int dtype, const void* in, int V, int R, int Cc, int Cin,
                                   const void* w, int Cout, int ldw, int s, const float* bias, void* out) {
   return guard(C(ctx), [&] {
-    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
     Lin l;
     l.w = const_cast<void*>(w);
     l.ldw = ldw;
     l.N = s * s * Cout;
     l.K = Cin;
     l.b = const_cast<float*>(bias);
-    GemmArgs u = lin_args(l, dtype == SPLAT_F32 ? F32 : BF16, in, Cin, V * R * Cc, out, 0);
+    GemmArgs u = lin_args(l, model_dtype(dtype), in, Cin, V * R * Cc, out, 0);
     u.store = STORE_CONVT;
     u.V = V;
     u.ct_s = s;
@@ -566,8 +559,7 @@ int splat_kernel_conv_transpose2d(splat_ctx* ctx, int dtype, const void* in, int
 int splat_kernel_resize_bilinear(splat_ctx* ctx, int dtype, const void* in, int V, int Hi, int Wi, int Cc, void* out,
                                  int Ho, int Wo) {
   return guard(C(ctx), [&] {
-    SPLAT_CHECK(dtype == SPLAT_F32 || dtype == SPLAT_BF16, BAD_ARGUMENT, "dtype");
-    resize_bilinear(C(ctx)->ex, dtype == SPLAT_F32 ? F32 : BF16, in, V, Hi, Wi, Cc, out, Ho, Wo, Ho, Wo, nullptr, 0);
+    resize_bilinear(C(ctx)->ex, model_dtype(dtype), in, V, Hi, Wi, Cc, out, Ho, Wo, Ho, Wo, nullptr, 0);
   });
 }
 

@@ -26,6 +26,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16> {
@@ -42,6 +43,13 @@ template <> struct Mfma<bf16> {
       w[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(short2_t, w[i]), short2_t{0, 0}));
     return v;
   }
+};
+template <> struct Mfma<f16> {
+  __device__ static inline void mma(f32x16& acc, const uint4& a, const uint4& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                 acc, 0, 0, 0);
+  }
+  __device__ static inline uint4 relu(uint4 v) { return Mfma<bf16>::relu(v); }  // same sign-bit rule
 };
 template <> struct Mfma<float> {
   // One 64-byte k-step of a 32x32 tile as 2 x 2 halves of 16 rows / 16 columns: a0, a1 the A
@@ -95,8 +103,8 @@ __device__ inline float gelu_erf(float x) {
 // A residual is fp32 when flagged, else stored in the kernel's own dtype T.
 template <typename T>
 __device__ inline float load_res(const void* p, long i, int f32) {
-  if (f32 || sizeof(T) == 4) return reinterpret_cast<const float*>(p)[i];
-  return bf2f(reinterpret_cast<const bf16*>(p)[i]);
+  if constexpr (sizeof(T) == 4) return reinterpret_cast<const float*>(p)[i];
+  else return f32 ? reinterpret_cast<const float*>(p)[i] : u16f<T>(reinterpret_cast<const uint16_t*>(p)[i]);
 }
 
 // Output index of element (m, n): row-major with optional row remap, or the transposed-conv
@@ -111,18 +119,20 @@ __device__ inline long out_index(const GemmArgs& p, long m, long n, long row) {
   return ((vv * p.ct_R * p.ct_s + rr * p.ct_s + dy) * ((long)p.ct_C * p.ct_s) + cc * p.ct_s + dx) * p.ct_Cout + co;
 }
 
+// 8 consecutive values, fp32 or (f32 false) the 16-bit type T.
+template <typename T>
 __device__ inline void load8(const void* p, long i, bool f32, float* v) {
-  if (f32) {
+  if (f32 || sizeof(T) == 4) {
     const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
     const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i + 4);
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(p) + i);
+  } else if constexpr (sizeof(T) == 2) {
+    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + i);
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      v[2 * k] = bf2f(bf16(w[k] & 0xffffu));
-      v[2 * k + 1] = bf2f(bf16(w[k] >> 16));
+      v[2 * k] = u16f<T>(w[k]);
+      v[2 * k + 1] = u16f<T>(w[k] >> 16);
     }
   }
 }
@@ -134,13 +144,13 @@ __device__ inline void store8_to(void* base, bool f32, const float* v, long idx)
     float* o = reinterpret_cast<float*>(base) + idx;
     *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
     *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
-  } else {
+  } else if constexpr (sizeof(T) == 2) {
     uint4 u;
-    u.x = pack_bf16x2(v[0], v[1]);
-    u.y = pack_bf16x2(v[2], v[3]);
-    u.z = pack_bf16x2(v[4], v[5]);
-    u.w = pack_bf16x2(v[6], v[7]);
-    *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(base) + idx) = u;
+    u.x = pack2<T>(v[0], v[1]);
+    u.y = pack2<T>(v[2], v[3]);
+    u.z = pack2<T>(v[4], v[5]);
+    u.w = pack2<T>(v[6], v[7]);
+    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(base) + idx) = u;
   }
 }
 // Store of 8 consecutive output values.
@@ -158,13 +168,13 @@ __device__ inline void epi8(const GemmArgs& p, float* v, long m, long n, bool ve
   const bool rf = p.res_f32 || sizeof(T) == 4, rf2 = p.res2_f32 || sizeof(T) == 4;
   if (vec) {
     float t[8];
-    if (p.bias) { load8(p.bias, n, true, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    if (p.bias) { load8<T>(p.bias, n, true, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
     if (p.act == ACT_RELU) for (int k = 0; k < 8; ++k) v[k] = fmaxf(v[k], 0.f);
     else if (p.act == ACT_GELU) for (int k = 0; k < 8; ++k) v[k] = gelu_erf(v[k]);
-    if (p.addtab) { load8(p.addtab, (m % p.addtab_period) * p.N + n, true, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
-    if (p.gamma) { load8(p.gamma, n, true, t); for (int k = 0; k < 8; ++k) v[k] *= t[k]; }
-    if (p.res) { load8(p.res, row * p.ldres + n, rf, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
-    if (p.res2) { load8(p.res2, row * p.ldres2 + n, rf2, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    if (p.addtab) { load8<T>(p.addtab, (m % p.addtab_period) * p.N + n, true, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    if (p.gamma) { load8<T>(p.gamma, n, true, t); for (int k = 0; k < 8; ++k) v[k] *= t[k]; }
+    if (p.res) { load8<T>(p.res, row * p.ldres + n, rf, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
+    if (p.res2) { load8<T>(p.res2, row * p.ldres2 + n, rf2, t); for (int k = 0; k < 8; ++k) v[k] += t[k]; }
     if (p.act_post == ACT_GELU) for (int k = 0; k < 8; ++k) v[k] = gelu_erf(v[k]);
     else if (p.act_post == ACT_RELU) for (int k = 0; k < 8; ++k) v[k] = fmaxf(v[k], 0.f);
     store8<T>(p, v, out_index(p, m, n, row));
@@ -397,9 +407,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
     float cb[8], cg[8], c1[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) { cb[k] = 0.f; cg[k] = 1.f; c1[k] = 0.f; }
-    if (nok && p.bias) load8(p.bias, n, true, cb);
-    if (RES && nok && p.gamma) load8(p.gamma, n, true, cg);
-    if (EPI == EPI_LN && nok) load8(p.ln_c1, n, true, c1);
+    if (nok && p.bias) load8<T>(p.bias, n, true, cb);
+    if (RES && nok && p.gamma) load8<T>(p.gamma, n, true, cg);
+    if (EPI == EPI_LN && nok) load8<T>(p.ln_c1, n, true, c1);
     const bool rf = p.res_f32 || sizeof(T) == 4, rf2 = p.res2_f32 || sizeof(T) == 4;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -421,7 +431,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
           const int rr = rsub + (t0 + t) * (64 / RUNS);
           const long m = wrow0 + i * 32 + rr;
           read8(slab + rr * LD + cc, v[t]);
-          if (RES && p.res && nok && m < p.M) load8(p.res, m * p.ldres + n, rf, rv[t]);
+          if (RES && p.res && nok && m < p.M) load8<T>(p.res, m * p.ldres + n, rf, rv[t]);
         }
         if (RES && p.res2) {  // second residual (the DPT residual units' skip input)
 #pragma unroll
@@ -429,7 +439,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
             const long m = wrow0 + i * 32 + rsub + (t0 + t) * (64 / RUNS);
             float r2[8];
             if (nok && m < p.M) {
-              load8(p.res2, m * p.ldres2 + n, rf2, r2);
+              load8<T>(p.res2, m * p.ldres2 + n, rf2, r2);
 #pragma unroll
               for (int k = 0; k < 8; ++k) rv[t][k] += r2[k];
             }
@@ -563,7 +573,7 @@ __device__ __forceinline__ void head_epilogue(const GemmArgs& p, f32x16 (&acc)[T
       float s[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const float h = bf2f(f2bf(fmaxf(v[k] + cb[k], 0.f)));
+        const float h = to_f<T>(from_f<T>(fmaxf(v[k] + cb[k], 0.f)));
 #pragma unroll
         for (int o = 0; o < 6; ++o) s[o] = fmaf(wt[o][k], h, s[o]);
       }
@@ -1350,7 +1360,9 @@ static bool launch_f32_auto(const Exec& ex, const GemmArgs& a) {
   }
 }
 
-static bool launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
+// The 16-bit types (bf16, f16) share the tile configurations.
+template <typename H>
+static bool launch_h16_auto(const Exec& ex, const GemmArgs& a) {
   const BfCfg c = pick_bf16(a);
   int S = split_factor(a, c);
   if (S > 1 && !(ex.ws && ex.ws->ptr && ex.ws->cap >= split_bytes(a, S))) S = 1;
@@ -1359,23 +1371,23 @@ static bool launch_bf16_auto(const Exec& ex, const GemmArgs& a) {
   // (256x256 with a third stage, so that the epilogue slabs fit the ring)
   if (a.amode == A_CONV && a.Cin % 64 != 0 && a.Cin % 32 == 0 && a.ks * a.ks <= 32 && !a.hw3) {
     switch (c) {
-      case CFG_128x64: return launch_mfma<bf16, 128, 64, 2, 2, 2, 32, 1, true>(ex, a, S);
-      case CFG_256x256: return launch_mfma<bf16, 256, 256, 2, 4, 3, 32, 1, true>(ex, a, S);
-      case CFG_256x128: return launch_mfma<bf16, 256, 128, 4, 2, 3, 32, 1, true>(ex, a, S);
-      case CFG_128x128: return launch_mfma<bf16, 128, 128, 2, 2, 4, 32, 1, true>(ex, a, S);
+      case CFG_128x64: return launch_mfma<H, 128, 64, 2, 2, 2, 32, 1, true>(ex, a, S);
+      case CFG_256x256: return launch_mfma<H, 256, 256, 2, 4, 3, 32, 1, true>(ex, a, S);
+      case CFG_256x128: return launch_mfma<H, 256, 128, 4, 2, 3, 32, 1, true>(ex, a, S);
+      case CFG_128x128: return launch_mfma<H, 128, 128, 2, 2, 4, 32, 1, true>(ex, a, S);
       default: break;  // 320- and 192-row and 32-column tiles: the per-lane path
     }
   }
   switch (c) {
-    case CFG_128x32: return launch_mfma<bf16, 128, 32, 4, 1, 2>(ex, a, S);
-    case CFG_128x64: return launch_mfma<bf16, 128, 64, 2, 2, 2>(ex, a, S);
-    case CFG_256x256: return launch_mfma<bf16, 256, 256, 2, 4, 2>(ex, a, S);
-    case CFG_256x128: return launch_mfma<bf16, 256, 128, 4, 2, 3>(ex, a, S);
-    case CFG_320x256: return launch_mfma<bf16, 320, 256, 2, 4, 2>(ex, a, S);
-    case CFG_320x128: return launch_mfma<bf16, 320, 128, 2, 4, 2>(ex, a, S);
-    case CFG_192x128: return launch_mfma<bf16, 192, 128, 2, 4, 3>(ex, a, S);
-    case CFG_192x128D: return launch_mfma<bf16, 192, 128, 2, 4, 2, 64, 2>(ex, a, S);
-    default: return launch_mfma<bf16, 128, 128, 2, 2, 4>(ex, a, S);
+    case CFG_128x32: return launch_mfma<H, 128, 32, 4, 1, 2>(ex, a, S);
+    case CFG_128x64: return launch_mfma<H, 128, 64, 2, 2, 2>(ex, a, S);
+    case CFG_256x256: return launch_mfma<H, 256, 256, 2, 4, 2>(ex, a, S);
+    case CFG_256x128: return launch_mfma<H, 256, 128, 4, 2, 3>(ex, a, S);
+    case CFG_320x256: return launch_mfma<H, 320, 256, 2, 4, 2>(ex, a, S);
+    case CFG_320x128: return launch_mfma<H, 320, 128, 2, 4, 2>(ex, a, S);
+    case CFG_192x128: return launch_mfma<H, 192, 128, 2, 4, 3>(ex, a, S);
+    case CFG_192x128D: return launch_mfma<H, 192, 128, 2, 4, 2, 64, 2>(ex, a, S);
+    default: return launch_mfma<H, 128, 128, 2, 2, 4>(ex, a, S);
   }
 }
 
@@ -1398,7 +1410,10 @@ static bool mfma_path_ok(const GemmArgs& a) {
 
 template <typename T>
 static bool launch_typed(const Exec& ex, const GemmArgs& a) {
-  if (mfma_path_ok(a)) return sizeof(T) == 2 ? launch_bf16_auto(ex, a) : launch_f32_auto(ex, a);
+  if (mfma_path_ok(a)) {
+    if constexpr (sizeof(T) == 2) return launch_h16_auto<T>(ex, a);
+    else return launch_f32_auto(ex, a);
+  }
   SPLAT_CHECK(a.hw3 == nullptr && a.ln_in == nullptr, BAD_ARGUMENT,
               "gemm: the fused head and the folded LayerNorm need the MFMA path");
   const long tiles128 = (long)cdiv(a.M, 128) * cdiv(a.N, 128);
@@ -1459,7 +1474,7 @@ void gemm(const Exec& ex, const GemmArgs& args) {
   bool stats;
   {
     ProfScope ps(ex, a.amode == A_ROWS ? "gemm" : "conv_igemm", 2.0 * mn * a.K, bytes);
-    stats = a.dt == F32 ? launch_typed<float>(ex, a) : launch_typed<bf16>(ex, a);
+    stats = a.dt == F32 ? launch_typed<float>(ex, a) : a.dt == F16 ? launch_typed<f16>(ex, a) : launch_typed<bf16>(ex, a);
   }
   if (a.ln_out && !stats)  // this path's epilogue does not emit them
     ln_stats(ex, static_cast<const float*>(a.out), a.ldc, a.M, a.N, a.ln_group, a.ln_out, a.dt, a.ln_copy);

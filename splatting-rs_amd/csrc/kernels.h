@@ -7,7 +7,7 @@
 
 namespace splat {
 
-enum Dtype { F32 = 0, BF16 = 1 };
+enum Dtype { F32 = 0, BF16 = 1, F16 = 2 };  // the C API's splat_dtype values
 inline size_t dtype_size(int dt) { return dt == F32 ? 4 : 2; }
 
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };

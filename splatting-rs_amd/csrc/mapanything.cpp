@@ -320,7 +320,7 @@ void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_o
     resize_bilinear(ex, dt_, h1, V, FH, FW, F / 2, up, H, W, H, W, nullptr, 0);
     GemmArgs g = conv_args(head2_, dt_, up, V, H, W, 1, nullptr);
     g.act = ACT_RELU;
-    if (dt_ == BF16 && F / 2 == 128 && head2_.cin % 64 == 0) {
+    if (dt_ != F32 && F / 2 == 128 && head2_.cin % 64 == 0) {
       // 1x1 head and dense_output in the convolution's epilogue: the 128-channel map at full
       // resolution (312 MB at C4) is never written
       g.out = up;  // not written

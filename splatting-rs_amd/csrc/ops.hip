@@ -37,7 +37,16 @@ __device__ inline double wave_sum_d(double v) {
   return v;
 }
 
-inline int in_dt_ok(int dt) { return dt == F32 || dt == BF16; }
+inline int in_dt_ok(int dt) { return dt == F32 || dt == BF16 || dt == F16; }
+
+// Calls f with a value of Ty<T> for the element type T of dtype dt (float, bf16 or f16).
+template <typename T> struct Ty { using type = T; };
+template <typename F> inline void by_dt(int dt, F&& f) {
+  if (dt == F32) f(Ty<float>{});
+  else if (dt == F16) f(Ty<f16>{});
+  else f(Ty<bf16>{});
+}
+#define TY(t) typename decltype(t)::type
 
 }  // namespace
 
@@ -67,21 +76,20 @@ __global__ void ln_kernel(const void* in, long ldin, void* out, long ldout, int 
   }
 }
 
-// 4 consecutive elements as floats / from floats (16-byte fp32 or 8-byte bf16 accesses).
-template <typename T> __device__ inline float4 ld4(const void* p, long i);
-template <> __device__ inline float4 ld4<float>(const void* p, long i) {
-  return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+// 4 consecutive elements as floats / from floats (16-byte fp32 or 8-byte bf16/f16 accesses).
+template <typename T> __device__ inline float4 ld4(const void* p, long i) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+  } else {
+    const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + i);
+    return make_float4(u16f<T>(u.x), u16f<T>(u.x >> 16), u16f<T>(u.y), u16f<T>(u.y >> 16));
+  }
 }
-template <> __device__ inline float4 ld4<bf16>(const void* p, long i) {
-  const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16*>(p) + i);
-  return make_float4(bf2f(bf16(u.x & 0xffffu)), bf2f(bf16(u.x >> 16)), bf2f(bf16(u.y & 0xffffu)), bf2f(bf16(u.y >> 16)));
-}
-template <typename T> __device__ inline void st4(void* p, long i, float4 v);
-template <> __device__ inline void st4<float>(void* p, long i, float4 v) {
-  *reinterpret_cast<float4*>(reinterpret_cast<float*>(p) + i) = v;
-}
-template <> __device__ inline void st4<bf16>(void* p, long i, float4 v) {
-  *reinterpret_cast<uint2*>(reinterpret_cast<bf16*>(p) + i) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+template <typename T> __device__ inline void st4(void* p, long i, float4 v) {
+  if constexpr (sizeof(T) == 4)
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(p) + i) = v;
+  else
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p) + i) = make_uint2(pack2<T>(v.x, v.y), pack2<T>(v.z, v.w));
 }
 
 // Register-resident LayerNorm: one wave per row, 4-element vector accesses, the row held in
@@ -152,10 +160,9 @@ void layer_norm(const Exec& ex, int in_dt, const void* in, long ldin, int out_dt
   SPLAT_CHECK((w == nullptr) == (b == nullptr), BAD_ARGUMENT, "layer_norm: weight and bias come together");
   if (ex.dry || rows == 0) return;
   ProfScope ps(ex, "layer_norm", 0, double(rows) * n * (dtype_size(in_dt) + dtype_size(out_dt)));
-  if (in_dt == F32 && out_dt == F32) ln_launch<float, float>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
-  else if (in_dt == F32) ln_launch<float, bf16>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
-  else if (out_dt == F32) ln_launch<bf16, float>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
-  else ln_launch<bf16, bf16>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off);
+  by_dt(in_dt, [&](auto ti) {
+    by_dt(out_dt, [&](auto to) { ln_launch<TY(ti), TY(to)>(ex, in, ldin, out, ldout, rows, n, w, b, eps, rm_P, rm_n, rm_off); });
+  });
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -203,8 +210,9 @@ void ln_stats(const Exec& ex, const float* x, long ldx, int rows, int n, int gro
   if (ex.dry || rows == 0) return;
   ProfScope ps(ex, "ln_stats", 0, double(rows) * n * (4 + (copy ? dtype_size(copy_dt) : 0)));
   dim3 grid(cdiv(rows, 4));
-  if (copy_dt == F32) hipLaunchKernelGGL(ln_stats_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, rows, n, group, stats, copy, rm_P, rm_n, rm_off);
-  else hipLaunchKernelGGL(ln_stats_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, rows, n, group, stats, copy, rm_P, rm_n, rm_off);
+  by_dt(copy_dt, [&](auto t) {
+    hipLaunchKernelGGL(ln_stats_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, x, ldx, rows, n, group, stats, copy, rm_P, rm_n, rm_off);
+  });
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -233,8 +241,7 @@ void im2col_patch(const Exec& ex, int dt, const float* img, int V, int H, int W,
   const long total = (long)V * (H / 14) * (W / 14) * kpad;
   ProfScope ps(ex, "im2col_patch", 0, double(V) * 3 * H * W * 4 + double(total) * dtype_size(dt));
   dim3 grid(cdiv(total, 256));
-  if (dt == F32) hipLaunchKernelGGL(im2col_kernel<float>, grid, dim3(256), 0, ex.stream, img, V, H, W, out, kpad);
-  else hipLaunchKernelGGL(im2col_kernel<bf16>, grid, dim3(256), 0, ex.stream, img, V, H, W, out, kpad);
+  by_dt(dt, [&](auto t) { hipLaunchKernelGGL(im2col_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, img, V, H, W, out, kpad); });
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -284,31 +291,30 @@ __global__ void resize_kernel(const void* in, int V, int Hi, int Wi, int C, void
 }
 
 // Same, 8 channels per thread (C % 8 == 0): the four source pixels and the output are read
-// and written as 8-channel vectors (one 16-byte access per pixel for bf16). One block row per
+// and written as 8-channel vectors (one 16-byte access per pixel for bf16 and f16). One block row per
 // output row (grid.y = V*Ho), so the row's source rows and weight follow from blockIdx.y and the
 // per-thread index math is 32-bit (C4's five resizes 295 -> 230 us against a flat 64-bit index
 // decomposition with 8-byte accesses). A thread covers RESIZE_ROWS output rows of one column, so
 // the column's source coordinate is computed once; coordinates are f64 products with the scale
 // (in - 1) / (out - 1) computed on the host (the f64 division per thread and row was most of
 // the kernel's instructions).
-template <typename T> struct Vec8;
-template <> struct Vec8<bf16> {
+template <typename T> struct Vec8 {  // the 16-bit types
   __device__ static inline void load(const void* p, long i, float* v) {
-    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(p) + i);
+    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + i);
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      v[2 * k] = bf2f(bf16(w[k] & 0xffffu));
-      v[2 * k + 1] = bf2f(bf16(w[k] >> 16));
+      v[2 * k] = u16f<T>(w[k]);
+      v[2 * k + 1] = u16f<T>(w[k] >> 16);
     }
   }
   __device__ static inline void store(void* p, long i, const float* v) {
     uint4 u;
-    u.x = pack_bf16x2(v[0], v[1]);
-    u.y = pack_bf16x2(v[2], v[3]);
-    u.z = pack_bf16x2(v[4], v[5]);
-    u.w = pack_bf16x2(v[6], v[7]);
-    *reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(p) + i) = u;
+    u.x = pack2<T>(v[0], v[1]);
+    u.y = pack2<T>(v[2], v[3]);
+    u.z = pack2<T>(v[4], v[5]);
+    u.w = pack2<T>(v[6], v[7]);
+    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p) + i) = u;
   }
 };
 template <> struct Vec8<float> {
@@ -377,15 +383,17 @@ void resize_bilinear(const Exec& ex, int dt, const void* in, int V, int Hi, int 
     SPLAT_CHECK(long(Wo) * (C / 8) < (1L << 31) && cdiv(rows, RESIZE_ROWS) < 65536, BAD_ARGUMENT, "resize: grid");
     const double sy = Hf > 1 ? double(Hi - 1) / double(Hf - 1) : 0.0, sx = Wf > 1 ? double(Wi - 1) / double(Wf - 1) : 0.0;
     dim3 grid(cdiv(long(Wo) * (C / 8), 256), cdiv(rows, RESIZE_ROWS));
-    if (dt == F32) hipLaunchKernelGGL(resize8_kernel<float>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Ho, Wo, rows, sy, sx, addtab, relu);
-    else hipLaunchKernelGGL(resize8_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Ho, Wo, rows, sy, sx, addtab, relu);
+    by_dt(dt, [&](auto t) {
+      hipLaunchKernelGGL(resize8_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, in, Hi, Wi, C, out, Ho, Wo, rows, sy, sx, addtab, relu);
+    });
     SPLAT_HIP(hipGetLastError());
     return;
   }
   ProfScope ps(ex, "resize_bilinear", 0, (double(V) * Hi * Wi * C + double(total)) * dtype_size(dt) + (addtab ? double(Ho) * Wo * C * 4 : 0));
   dim3 grid(cdiv(total, 256));
-  if (dt == F32) hipLaunchKernelGGL(resize_kernel<float>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
-  else hipLaunchKernelGGL(resize_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+  by_dt(dt, [&](auto t) {
+    hipLaunchKernelGGL(resize_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, in, V, Hi, Wi, C, out, Hf, Wf, Ho, Wo, addtab, relu);
+  });
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -584,10 +592,9 @@ void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, 
     ProfScope ps(ex, "pointwise_head", 2.0 * pix * cin * cout, double(pix) * (cin * dtype_size(dt) + obytes));
     // about three 256-thread blocks per CU, each lane group walking many pixels
     const long blocks = std::min<long>(cdiv(pix * 8, 256), 256L * 3);
-    if (dt == F32)
-      hipLaunchKernelGGL(pw_ma128_kernel<float>, dim3(blocks), dim3(256), 0, ex.stream, in, pix, hw, w, b, o0, o1, o2, o3, scale);
-    else
-      hipLaunchKernelGGL(pw_ma128_kernel<bf16>, dim3(blocks), dim3(256), 0, ex.stream, in, pix, hw, w, b, o0, o1, o2, o3, scale);
+    by_dt(dt, [&](auto t) {
+      hipLaunchKernelGGL(pw_ma128_kernel<TY(t)>, dim3(blocks), dim3(256), 0, ex.stream, in, pix, hw, w, b, o0, o1, o2, o3, scale);
+    });
     SPLAT_HIP(hipGetLastError());
     return;
   }
@@ -600,11 +607,9 @@ void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, 
     const int lpp = cin / 8;
     dim3 grid(cdiv(pix * lpp, 256));
 #define PWC(T, L) hipLaunchKernelGGL((pw_coop_kernel<T, L>), grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale)
-    if (dt == F32) {
-      if (lpp == 4) PWC(float, 4); else if (lpp == 8) PWC(float, 8); else PWC(float, 16);
-    } else {
-      if (lpp == 4) PWC(bf16, 4); else if (lpp == 8) PWC(bf16, 8); else PWC(bf16, 16);
-    }
+    by_dt(dt, [&](auto t) {
+      if (lpp == 4) PWC(TY(t), 4); else if (lpp == 8) PWC(TY(t), 8); else PWC(TY(t), 16);
+    });
 #undef PWC
     SPLAT_HIP(hipGetLastError());
     return;
@@ -616,8 +621,9 @@ void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, 
   const double obytes = mode == PW_MA ? (o0 ? 24.0 : 0) + (o1 ? 12.0 : 0) + (o2 ? 4.0 : 0) + (o3 ? 1.0 : 0) : 4.0 * cout;
   ProfScope ps(ex, "pointwise_head", 2.0 * pix * cin * cout, double(pix) * (cin * dtype_size(dt) + obytes));
   dim3 grid(cdiv(pix, 256));
-  if (dt == F32) hipLaunchKernelGGL(pw_kernel<float>, grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale);
-  else hipLaunchKernelGGL(pw_kernel<bf16>, grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale);
+  by_dt(dt, [&](auto t) {
+    hipLaunchKernelGGL(pw_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, mode, in, pix, hw, cin, cout, w, b, o0, o1, o2, o3, scale);
+  });
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -625,14 +631,13 @@ void pointwise_head(const Exec& ex, int dt, int mode, const void* in, long pix, 
 // Small linears for the heads: one wave per output column n. Each lane takes 8 consecutive k
 // at a time (one 16-byte weight load) and keeps the partial sums of up to 8 rows, so the weight
 // row is read once for all rows.
-template <typename TW> __device__ inline void load_w8(const void* W, long i, float* w);
-template <> __device__ inline void load_w8<bf16>(const void* W, long i, float* w) {
-  const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(W) + i);
+template <typename TW> __device__ inline void load_w8(const void* W, long i, float* w) {  // the 16-bit types
+  const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(W) + i);
   const uint32_t q[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    w[2 * k] = bf2f(bf16(q[k] & 0xffffu));
-    w[2 * k + 1] = bf2f(bf16(q[k] >> 16));
+    w[2 * k] = u16f<TW>(q[k]);
+    w[2 * k + 1] = u16f<TW>(q[k] >> 16);
   }
 }
 template <> __device__ inline void load_w8<float>(const void* W, long i, float* w) {
@@ -702,11 +707,13 @@ void small_linear(const Exec& ex, int wdt, const float* x, long ldx, int M, int 
   const bool vec = K % 8 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(W) & 15) == 0 && (ldw * dtype_size(wdt)) % 16 == 0;
   if (vec) {
-    if (wdt == F32) hipLaunchKernelGGL(small_linear8_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
-    else hipLaunchKernelGGL(small_linear8_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+    by_dt(wdt, [&](auto t) {
+      hipLaunchKernelGGL(small_linear8_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+    });
   } else {
-    if (wdt == F32) hipLaunchKernelGGL(small_linear_kernel<float>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
-    else hipLaunchKernelGGL(small_linear_kernel<bf16>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+    by_dt(wdt, [&](auto t) {
+      hipLaunchKernelGGL(small_linear_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, x, ldx, M, K, W, ldw, b, y, ldy, N, act);
+    });
   }
   SPLAT_HIP(hipGetLastError());
 }
@@ -878,8 +885,9 @@ void da3_hook(const Exec& ex, int dt, const float* within, const float* xs, int 
   if (ex.dry) return;
   ProfScope ps(ex, "da3_hook", 0, double(V) * n * dim * 8 + double(V) * (n - 1) * 2 * dim * dtype_size(dt));
   dim3 grid(cdiv((long)V * n, 4));
-  if (dt == F32) hipLaunchKernelGGL(da3_hook_kernel<float>, grid, dim3(256), 0, ex.stream, within, xs, V, n, dim, bnw, bnb, hnw, hnb, out, cam_out);
-  else hipLaunchKernelGGL(da3_hook_kernel<bf16>, grid, dim3(256), 0, ex.stream, within, xs, V, n, dim, bnw, bnb, hnw, hnb, out, cam_out);
+  by_dt(dt, [&](auto t) {
+    hipLaunchKernelGGL(da3_hook_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, within, xs, V, n, dim, bnw, bnb, hnw, hnb, out, cam_out);
+  });
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -893,10 +901,12 @@ __global__ void convert_kernel(const void* in, void* out, long count) {
 void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count) {
   if (ex.dry || count == 0) return;
   dim3 grid(cdiv(count, 256));
-  if (in_dt == F32 && out_dt == BF16) hipLaunchKernelGGL((convert_kernel<float, bf16>), grid, dim3(256), 0, ex.stream, in, out, count);
-  else if (in_dt == BF16 && out_dt == F32) hipLaunchKernelGGL((convert_kernel<bf16, float>), grid, dim3(256), 0, ex.stream, in, out, count);
-  else if (in_dt == F32) hipLaunchKernelGGL((convert_kernel<float, float>), grid, dim3(256), 0, ex.stream, in, out, count);
-  else hipLaunchKernelGGL((convert_kernel<bf16, bf16>), grid, dim3(256), 0, ex.stream, in, out, count);
+  SPLAT_CHECK(in_dt_ok(in_dt) && in_dt_ok(out_dt), BAD_ARGUMENT, "convert: dtype");
+  by_dt(in_dt, [&](auto ti) {
+    by_dt(out_dt, [&](auto to) {
+      hipLaunchKernelGGL((convert_kernel<TY(ti), TY(to)>), grid, dim3(256), 0, ex.stream, in, out, count);
+    });
+  });
   SPLAT_HIP(hipGetLastError());
 }
 
@@ -1029,16 +1039,14 @@ void mean_rows(const Exec& ex, int dt, const void* in, int groups, int P, int C,
   if (two_pass && ex.ws->ptr && ex.ws->cap >= pbytes) {
     float* part = static_cast<float*>(ex.ws->ptr);
     dim3 grid(groups, cdiv(C / 8, 64), MEAN_SLICES);
-    if (dt == F32) hipLaunchKernelGGL(mean_rows_part_kernel<float>, grid, dim3(256), 0, ex.stream, in, P, C, part);
-    else hipLaunchKernelGGL(mean_rows_part_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, P, C, part);
+    by_dt(dt, [&](auto t) { hipLaunchKernelGGL(mean_rows_part_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, in, P, C, part); });
     SPLAT_HIP(hipGetLastError());
     hipLaunchKernelGGL(mean_rows_final_kernel, dim3(cdiv(groups * C, 256)), dim3(256), 0, ex.stream, part, groups, P, C, out);
     SPLAT_HIP(hipGetLastError());
     return;
   }
   dim3 grid(groups, cdiv(C, 64));
-  if (dt == F32) hipLaunchKernelGGL(mean_rows_kernel<float>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
-  else hipLaunchKernelGGL(mean_rows_kernel<bf16>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out);
+  by_dt(dt, [&](auto t) { hipLaunchKernelGGL(mean_rows_kernel<TY(t)>, grid, dim3(256), 0, ex.stream, in, groups, P, C, out); });
   SPLAT_HIP(hipGetLastError());
 }
 

@@ -96,11 +96,15 @@ Lin Loader::pack(std::vector<float>& rows, int n, int k, float* bias, int dt) {
       for (size_t r = a; r < b; ++r) std::memcpy(&buf[r * l.ldw], &rows[r * k], sizeof(float) * k);
     });
     l.w = ctx_.pool.upload(buf.data(), total * 4);
-  } else {
-    std::vector<bf16> buf(total, 0);
+  } else {  // bf16 or f16, rounded to nearest even
+    std::vector<uint16_t> buf(total, 0);
+    const bool half = dt == F16;
     parallel_for(size_t(n), [&](size_t a, size_t b) {
       for (size_t r = a; r < b; ++r)
-        for (int c = 0; c < k; ++c) buf[r * l.ldw + c] = f2bf(rows[r * size_t(k) + c]);
+        for (int c = 0; c < k; ++c) {
+          const float v = rows[r * size_t(k) + c];
+          buf[r * l.ldw + c] = half ? f2h(v) : f2bf(v);
+        }
     });
     l.w = ctx_.pool.upload(buf.data(), total * 2);
   }
@@ -184,7 +188,8 @@ Lin Loader::linear_ln(const std::string& name, int n_out, int n_in, const std::s
       for (int k = 0; k < n_in; ++k) {
         sb += double(beta[k]) * row[k];
         row[k] *= g[k];
-        s1 += dt_ == F32 ? double(row[k]) : double(bf2f(f2bf(row[k])));  // the stored value
+        // the stored value
+        s1 += dt_ == F32 ? double(row[k]) : dt_ == F16 ? double(h2f(f2h(row[k]))) : double(bf2f(f2bf(row[k])));
       }
       c2[r] = float(sb);
       c1[r] = float(s1);
@@ -313,7 +318,7 @@ void block_forward(Context& ctx, const Block& b, int dt, const float* in, float*
       g.rope_npos = npos;
     }
   }
-  if (dt != F32) {  // Q leaves the epilogue times the softmax scale, rounded to bf16 once
+  if (dt != F32) {  // Q leaves the epilogue times the softmax scale, rounded to bf16 or f16 once
     g.q_cols = d;
     g.q_scale = ATTN_Q_SCALE;
   }

@@ -119,7 +119,7 @@ class BenchConfig:
     views: int
     height: int
     width: int
-    dtype: str            # "f32" or "bf16"
+    dtype: str            # "f32", "bf16" or "f16"
     images: str           # "uniform" or "procedural"
     brightness: bool = False
     encoder_only: bool = False

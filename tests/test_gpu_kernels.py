@@ -1,6 +1,10 @@
 """Kernel-level parity of the MFMA GEMM and the flash-attention kernel (through the C ABI's
 kernel entry points, include/splathip_kernels.h) against plain PyTorch fp32/fp64 references
-of the same op on the same bf16/fp32-rounded operands."""
+of the same op on the same bf16/f16/fp32-rounded operands.
+
+Bounds on a result stored in a 16-bit type are set by its rounding: half an ulp is 2^-9 of the
+value in bf16 (8 mantissa bits) and 2^-12 in f16 (11 bits), so the f16 bounds sit 4-8x below
+the bf16 ones."""
 import math
 
 import numpy as np
@@ -15,7 +19,15 @@ torch = pytest.importorskip("torch")
 
 def _dt(name):
     import splathip
-    return (splathip.BF16, torch.bfloat16) if name == "bf16" else (splathip.F32, torch.float32)
+    return {"bf16": (splathip.BF16, torch.bfloat16), "f16": (splathip.F16, torch.float16),
+            "f32": (splathip.F32, torch.float32)}[name]
+
+
+def _tol(dtype, f32, bf16, f16):
+    return {"f32": f32, "bf16": bf16, "f16": f16}[dtype]
+
+
+DTYPES = ["bf16", "f16", "f32"]
 
 
 GEMM_CASES = [
@@ -41,7 +53,7 @@ GEMM_CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M,N,K,act", GEMM_CASES)
 def test_gemm_matches_torch(ctx, dtype, M, N, K, act):
     report("gemm", dtype=dtype, M=M, N=N, K=K, act=act)
@@ -67,16 +79,16 @@ def test_gemm_matches_torch(ctx, dtype, M, N, K, act):
     err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
     report("gemm.err", err=f"{err:.2e}")
     assert err < (1e-5 if dtype == "f32" else 2e-5), err
-    # bf16/fp32 output storage path
+    # output stored in the operands' type
     out2 = torch.empty(M, N, dtype=tdt, device="cuda")
     torch.cuda.synchronize()  # inputs were written on torch's stream, the library runs on its own
     ctx.kernel_gemm(code, dA.data_ptr(), M, K, dW.data_ptr(), N, ldw, db.data_ptr(), act, out2.data_ptr(), False)
     ctx.synchronize()
     err2 = (out2.cpu().double() - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
-    assert err2 < (1e-5 if dtype == "f32" else 8e-3), err2
+    assert err2 < _tol(dtype, 1e-5, 8e-3, 1e-3), err2
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_gemm_gelu_epilogue_accuracy(ctx, dtype):
     """The epilogue's GELU against the exact erf GELU over [-9, 9]: out[m, n] = x_m (A's first
     column, W's first row of ones), so the GEMM adds no rounding and the check is the
@@ -119,7 +131,7 @@ ATTN_CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("S,L,heads", ATTN_CASES)
 def test_attention_matches_torch(ctx, dtype, S, L, heads):
     if dtype == "f32" and S * L > 6000:
@@ -140,18 +152,19 @@ def test_attention_matches_torch(ctx, dtype, S, L, heads):
     got = out.cpu().double()
     err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
     report("attention.err", err=f"{err:.2e}")
-    assert err < (2e-5 if dtype == "f32" else 2e-2), err
+    assert err < _tol(dtype, 2e-5, 2e-2, 4e-3), err
 
 
-# The bf16 kernel's softmax scale: Q times log2(e)/8 in fp32, rounded to bf16 (a second rounding
-# of Q when, as through splat_kernel_attention, Q arrives unscaled), then weights 2^(q'.k).
+# The 16-bit kernels' softmax scale: Q times log2(e)/8 in fp32, rounded to bf16 or f16 (a second
+# rounding of Q when, as through splat_kernel_attention, Q arrives unscaled), then weights
+# 2^(q'.k).
 Q_SCALE = float(np.float32(0.125) * np.float32(1.4426950408889634))
 
 
 def _attention_ref_scaled(dq, S, L, heads):
     x = dq.float().reshape(S, L, 3, heads, 64).permute(2, 0, 3, 1, 4)  # [3, S, h, L, 64]
     q = x[0] * np.float32(Q_SCALE)  # fp32: the kernel scales Q in fp32 and keeps it there
-    q = (q.bfloat16() if dq.dtype == torch.bfloat16 else q).double()
+    q = (q.to(dq.dtype) if dq.dtype != torch.float32 else q).double()
     p = torch.softmax((q @ x[1].double().transpose(-1, -2)) * math.log(2.0), -1)
     return (p @ x[2].double()).permute(0, 2, 1, 3).reshape(S * L, heads * 64).cpu()
 
@@ -161,11 +174,14 @@ def _attention_ref_scaled(dq, S, L, heads):
 # above the rest in a late tile, and a mix of queries in each regime. Shapes: one and two query
 # sub-tiles per wave, with and without key slices, ragged last tiles. At logits of hundreds the
 # rounding of Q alone moves them by units, so the reference follows the kernel's Q rounding and
-# the test checks the softmax and its reference moves, at the usual tolerance.
+# the test checks the softmax and its reference moves, at the usual tolerance. In f16 the kernel
+# keeps the running reference from the first tile (weights at most 2^8, inside f16's range);
+# "high" is the case whose weights 2^s would pass f16's 65504 without it.
 EXTREME_CASES = ["high", "low", "late_peak", "mixed"]
 
 
 @pytest.mark.parametrize("dtype,S,L,heads", [("bf16", 2, 1037, 3), ("bf16", 7, 1037, 16), ("bf16", 1, 6223, 2),
+                                             ("f16", 2, 1037, 3), ("f16", 7, 1037, 16), ("f16", 1, 6223, 2),
                                              ("f32", 1, 1297, 6), ("f32", 3, 130, 2)])
 @pytest.mark.parametrize("kind", EXTREME_CASES)
 def test_attention_extreme_logits(ctx, kind, dtype, S, L, heads):
@@ -201,7 +217,7 @@ def test_attention_extreme_logits(ctx, kind, dtype, S, L, heads):
     report("attention.extreme.err", err=f"{err:.2e}")
     # fp32: at logits near +600 (865 in base 2) fp32 holds the exponent itself to ~5e-5, so the
     # weights carry ~1e-4 relative error whatever the kernel does
-    assert err < (1e-3 if dtype == "f32" else 2e-2), err
+    assert err < _tol(dtype, 1e-3, 2e-2, 4e-3), err
 
 
 CONV_CASES = [
@@ -231,11 +247,11 @@ CONV_CASES = [
     (3, 112, 148, 96, 256, 3, 1, 0, 0, False),
     (3, 88, 94, 96, 256, 3, 1, 1, 1, True),
 ]
-BF16_ONLY = {(3, 112, 148, 96, 256), (3, 88, 94, 96, 256)}
+H16_ONLY = {(3, 112, 148, 96, 256), (3, 88, 94, 96, 256)}
 
 
 def bf16_tile(M, N, conv):
-    """The bf16 tile the library's picker (gemm.hip pick_bf16) chooses for an M x N launch:
+    """The 16-bit tile the library's picker (gemm.hip pick_bf16) chooses for an M x N launch:
     the fewest rounds of 256 CUs weighted by each tile's relative per-flop cost."""
     if N <= 32:
         return "128x32"
@@ -253,15 +269,15 @@ def bf16_tile(M, N, conv):
     return pick
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("V,H,W,Cin,Cout,ks,stride,relu_in,act,residual", CONV_CASES)
 def test_conv2d_matches_torch(ctx, dtype, V, H, W, Cin, Cout, ks, stride, relu_in, act, residual):
-    if dtype == "f32" and (V, H, W, Cin, Cout) in BF16_ONLY:
-        pytest.skip("a bf16 tile-path case (fp32 picks its own tiles)")
+    if dtype == "f32" and (V, H, W, Cin, Cout) in H16_ONLY:
+        pytest.skip("a 16-bit tile-path case (fp32 picks its own tiles)")
     pad = ks // 2
     Ho, Wo = (H + 2 * pad - ks) // stride + 1, (W + 2 * pad - ks) // stride + 1
     report("conv2d", dtype=dtype, V=V, H=H, W=W, Cin=Cin, Cout=Cout, ks=ks, stride=stride,
-           tile=bf16_tile(V * Ho * Wo, Cout, ks > 1) if dtype == "bf16" else "fp32")
+           tile=bf16_tile(V * Ho * Wo, Cout, ks > 1) if dtype != "f32" else "fp32")
     code, tdt = _dt(dtype)
     F = torch.nn.functional
     g = torch.Generator().manual_seed(V * 31 + H * 7 + Cin + Cout)
@@ -291,10 +307,10 @@ def test_conv2d_matches_torch(ctx, dtype, V, H, W, Cin, Cout, ks, stride, relu_i
     got = out.cpu().double().permute(0, 3, 1, 2)
     err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
     report("conv2d.err", err=f"{err:.2e}")
-    assert err < (1e-5 if dtype == "f32" else 8e-3), err
+    assert err < _tol(dtype, 1e-5, 8e-3, 1e-3), err
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("V,R,Cc,Cin,Cout,s", [(1, 3, 4, 48, 48, 4), (2, 27, 36, 96, 96, 2), (2, 5, 3, 32, 16, 4)])
 def test_conv_transpose2d_matches_torch(ctx, dtype, V, R, Cc, Cin, Cout, s):
     report("convT", dtype=dtype, V=V, R=R, C=Cc, Cin=Cin, Cout=Cout, s=s)
@@ -317,10 +333,10 @@ def test_conv_transpose2d_matches_torch(ctx, dtype, V, R, Cc, Cin, Cout, s):
     ctx.synchronize()
     got = out.cpu().double().permute(0, 3, 1, 2)
     err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
-    assert err < (1e-5 if dtype == "f32" else 8e-3), err
+    assert err < _tol(dtype, 1e-5, 8e-3, 1e-3), err
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("V,Hi,Wi,C,Ho,Wo", [(1, 4, 3, 8, 8, 6), (2, 14, 18, 64, 27, 36), (1, 224, 296, 32, 392, 518),
                                               (1, 1, 5, 4, 3, 10), (2, 7, 7, 16, 7, 7)])
 def test_resize_bilinear_matches_torch(ctx, dtype, V, Hi, Wi, C, Ho, Wo):
@@ -336,7 +352,7 @@ def test_resize_bilinear_matches_torch(ctx, dtype, V, Hi, Wi, C, Ho, Wo):
     ctx.synchronize()
     got = out.cpu().double().permute(0, 3, 1, 2)
     err = (got - ref).abs().max().item() / (ref.abs().max().item() + 1e-12)
-    assert err < (1e-6 if dtype == "f32" else 8e-3), err
+    assert err < _tol(dtype, 1e-6, 8e-3, 1e-3), err
 
 
 # --- LayerNorm folded into the block GEMMs (GemmArgs::ln_in / ln_out) ----------------------
@@ -364,13 +380,13 @@ LN_CONSUMER_CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M,N,K,act,group", LN_CONSUMER_CASES)
 def test_gemm_folded_layernorm_matches_torch(ctx, dtype, M, N, K, act, group):
     """act(LN(x) W^T + b) from the un-normalised rows, their statistics (ln_stats kernel) and the
     folded weights, rows with a non-zero mean so that the mean term matters: (1) the epilogue
     algebra against fp64 on the same rounded operands; (2) the whole fold against torch's
-    LayerNorm and linear in fp64 (bf16: the rounding of x and of W * gamma)."""
+    LayerNorm and linear in fp64 (bf16, f16: the rounding of x and of W * gamma)."""
     report("gemm_ln", dtype=dtype, M=M, N=N, K=K, act=act, group=group)
     code, tdt = _dt(dtype)
     g = torch.Generator().manual_seed(M + 5 * N + 11 * K)
@@ -387,7 +403,7 @@ def test_gemm_folded_layernorm_matches_torch(ctx, dtype, M, N, K, act, group):
     Wp[:, :K] = Wf
     dx = x.cuda()
     stats = torch.empty(M, K // group, 2, device="cuda")
-    copy = torch.empty(M, K, dtype=tdt, device="cuda") if dtype == "bf16" else None
+    copy = torch.empty(M, K, dtype=tdt, device="cuda") if dtype != "f32" else None
     dW, dc1, dc2 = Wp.cuda(), c1.cuda(), c2.cuda()
     out = torch.empty(M, N, device="cuda")
     torch.cuda.synchronize()
@@ -415,7 +431,7 @@ def test_gemm_folded_layernorm_matches_torch(ctx, dtype, M, N, K, act, group):
     err2 = (got - true).abs().max().item() / (true.abs().max().item() + 1e-12)
     report("gemm_ln.err", same_operands=f"{err:.2e}", vs_layer_norm=f"{err2:.2e}")
     assert err < 2e-5, err
-    assert err2 < (1e-5 if dtype == "f32" else 2e-2), err2
+    assert err2 < _tol(dtype, 1e-5, 2e-2, 4e-3), err2
 
 
 def test_gemm_split_k_repeat(ctx):
@@ -425,7 +441,7 @@ def test_gemm_split_k_repeat(ctx):
     call's result."""
     outs = {}
     shapes = [(1297, 384, 1536, "f32"), (100, 256, 4096, "bf16"), (777, 64, 2048, "f32"), (1297, 384, 1536, "f32"),
-              (300, 1001, 2048, "bf16"), (100, 256, 4096, "bf16")]
+              (300, 1001, 2048, "bf16"), (100, 256, 4096, "f16"), (100, 256, 4096, "bf16"), (300, 1001, 2048, "f16")]
     for M, N, K, dtype in shapes:
         code, tdt = _dt(dtype)
         g = torch.Generator().manual_seed(M + N + K)
@@ -466,7 +482,7 @@ LN_PRODUCER_CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M,N,K,group", LN_PRODUCER_CASES)
 def test_gemm_residual_statistics(ctx, dtype, M, N, K, group):
     """out = res + gamma * (A W^T + b) in fp32, the (sum, sum of squares) of every output row per
