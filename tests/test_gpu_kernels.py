@@ -43,6 +43,8 @@ GEMM_CASES = [
     (6000, 3072, 1024, 2),  # 320x256 tiles (228: one round of 256 CUs)
     (6000, 1536, 512, 1),   # 320x128 tiles (228)
     (6000, 768, 768, 0),    # 192x128 tiles (192)
+    # 400 tiles of 256x256: a second round of 144 tiles (the MapAnything encoder's fc1 shape)
+    (6222, 4096, 1024, 2),
     # split-K (fewer tiles than half a round of CUs, K >= 16 k-tiles): fp32 partials + reduce
     (100, 256, 4096, 0),
     (777, 64, 2048, 2),
@@ -246,8 +248,13 @@ CONV_CASES = [
     # and 256x128 with ReLU-on-load and a residual
     (3, 112, 148, 96, 256, 3, 1, 0, 0, False),
     (3, 88, 94, 96, 256, 3, 1, 1, 1, True),
+    # 389 tiles of 256x256 (the DPT heads' finest 256-channel maps, 6 x 112 x 148 pixels, 1.52
+    # rounds): per-tap path with ReLU-on-load and a residual, then Cin = 96 (32-element k-tiles)
+    # with bias + ReLU
+    (6, 112, 148, 128, 256, 3, 1, 1, 0, True),
+    (6, 112, 148, 96, 256, 3, 1, 0, 1, False),
 ]
-H16_ONLY = {(3, 112, 148, 96, 256), (3, 88, 94, 96, 256)}
+H16_ONLY = {(3, 112, 148, 96, 256), (3, 88, 94, 96, 256), (6, 112, 148, 128, 256), (6, 112, 148, 96, 256)}
 
 
 def bf16_tile(M, N, conv):
@@ -478,6 +485,7 @@ LN_PRODUCER_CASES = [
     (1297, 384, 1536, 64),    # DA3-Small C1 fc2: split-K, statistics from the ln_stats kernel
     (1297, 1536, 1536, 128),  # split-K, 128-column groups
     (1400, 1536, 1536, 128),  # reference-dims MapAnything proj (128-column groups)
+    (6222, 4096, 1024, 128),  # 400 tiles of 256x256 (1.56 rounds), 32 groups a row
     (200, 128, 64, 64),       # one row tile, ragged
 ]
 
@@ -518,3 +526,74 @@ def test_gemm_residual_statistics(ctx, dtype, M, N, K, group):
     assert err < (1e-5 if dtype == "f32" else 2e-5), err
     assert st_err < 1e-5, st_err
     assert torch.equal(copy.cpu(), got.to(tdt))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gemm_operand_beyond_2gib(ctx, dtype):
+    """An A operand of 2 GiB or more leaves the 32-bit buffer offsets of the MFMA path: the GEMM
+    runs on the register-staged kernel (gemm.hip gemm_kernel, 64-bit addresses). Rows sampled
+    at the start, across the 2 GiB boundary and at the ragged end against fp64."""
+    code, tdt = _dt(dtype)
+    es = 4 if dtype == "f32" else 2
+    K, N = 1024, 96
+    M = (1 << 31) // (K * es) + 37
+    report("gemm.2gib", dtype=dtype, M=M, N=N, K=K, A_bytes=M * K * es)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    A = torch.randn(M, K, device="cuda", dtype=tdt, generator=g)
+    Wm = torch.zeros(N, K, dtype=tdt)
+    Wm[:, :] = (torch.randn(N, K, generator=torch.Generator().manual_seed(8)) * 0.05).to(tdt)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(9))
+    dW, db = Wm.cuda(), b.cuda()
+    out = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.kernel_gemm(code, A.data_ptr(), M, K, dW.data_ptr(), N, K, db.data_ptr(), 1, out.data_ptr(), True)
+    ctx.synchronize()
+    # contiguous row ranges copied to the host (torch's gather kernel is not used on a tensor
+    # this large: its index arithmetic faults past 2 GiB)
+    half = (1 << 31) // (K * es)
+    err = 0.0
+    for r0, r1 in ((0, 64), (half - 64, half + 64), (M - 64, M)):
+        ref = torch.relu(A[r0:r1].cpu().double() @ Wm.double().T + b.double())
+        got = out[r0:r1].cpu().double()
+        err = max(err, ((got - ref).abs().max() / ref.abs().max()).item())
+    report("gemm.2gib.err", err=f"{err:.2e}")
+    assert err < 1e-5, err
+    del A, out
+    torch.cuda.empty_cache()
+
+
+def test_conv_input_beyond_2gib(ctx):
+    """A bf16 convolution whose input map is 2 GiB (2 views of 512 x 512 x 2048) runs on the
+    register-staged kernel; output pixels at the corners, edges and the map's far end against
+    fp64 sums over their 3 x 3 neighbourhoods (zero padding)."""
+    code, tdt = _dt("bf16")
+    V, H, W, Cin, Cout = 2, 512, 512, 2048, 48
+    report("conv2d.2gib", V=V, H=H, W=W, Cin=Cin, Cout=Cout, in_bytes=V * H * W * Cin * 2)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(V, H, W, Cin, device="cuda", dtype=tdt, generator=g)
+    K = 9 * Cin
+    w = (torch.randn(Cout, 3, 3, Cin, generator=torch.Generator().manual_seed(12)) * 0.02).to(tdt)
+    b = torch.randn(Cout, generator=torch.Generator().manual_seed(13))
+    dw, db = w.reshape(Cout, K).contiguous().cuda(), b.cuda()
+    out = torch.full((V, H, W, Cout), float("nan"), dtype=tdt, device="cuda")
+    torch.cuda.synchronize()
+    ctx.kernel_conv2d(code, x.data_ptr(), V, H, W, Cin, dw.data_ptr(), Cout, K, 3, 1, db.data_ptr(), 0, 0, 0,
+                      out.data_ptr())
+    ctx.synchronize()
+    pix = [(0, 0, 0), (0, 0, W - 1), (0, H - 1, 7), (0, 255, 300), (1, 0, 0), (1, 311, 0), (1, 200, 511),
+           (1, H - 1, W - 1), (1, H - 2, W - 3)]
+    wd = w.double()
+    err = 0.0
+    for v, y, xx in pix:
+        acc = b.double().clone()
+        for ky in range(3):
+            for kx in range(3):
+                iy, ix = y + ky - 1, xx + kx - 1
+                if 0 <= iy < H and 0 <= ix < W:
+                    acc += wd[:, ky, kx, :] @ x[v, iy, ix].cpu().double()
+        got = out[v, y, xx].cpu().double()
+        err = max(err, ((got - acc).abs() / (acc.abs() + 0.05 * acc.abs().max())).max().item())
+    report("conv2d.2gib.err", err=f"{err:.2e}")
+    assert err < 1e-2, err
+    del x, out
+    torch.cuda.empty_cache()
