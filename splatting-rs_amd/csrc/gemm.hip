@@ -415,8 +415,29 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
     if (RES && nok && p.gamma) load8<T>(p.gamma, n, true, cg);
     if (EPI == EPI_LN && nok) load8<T>(p.ln_c1, n, true, c1);
     const bool rf = p.res_f32 || sizeof(T) == 4, rf2 = p.res2_f32 || sizeof(T) == 4;
+    // The residual runs of slab i + 1 are requested while slab i is staged and stored, so that
+    // only the first slab's wait is exposed.
+    float rvn[IT][8];
+    auto load_res = [&](int i) {
+#pragma unroll
+      for (int t = 0; t < IT; ++t) {
+        const long m = wrow0 + i * 32 + rsub + t * (64 / RUNS);
+        if (RES && p.res && nok && m < p.M) load8<T>(p.res, m * p.ldres + n, rf, rvn[t]);
+        else if (RES) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) rvn[t][k] = 0.f;
+        }
+      }
+    };
+    load_res(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+      float rvs[IT][8];
+#pragma unroll
+      for (int t = 0; t < IT; ++t)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) rvs[t][k] = rvn[t][k];
+      if (i + 1 < TM) load_res(i + 1);
       float la[IT], lb[IT];  // folded LayerNorm of this lane's rows
       if constexpr (EPI == EPI_LN) {
 #pragma unroll
@@ -435,7 +456,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
           const int rr = rsub + (t0 + t) * (64 / RUNS);
           const long m = wrow0 + i * 32 + rr;
           read8(slab + rr * LD + cc, v[t]);
-          if (RES && p.res && nok && m < p.M) load8<T>(p.res, m * p.ldres + n, rf, rv[t]);
+          if (RES && p.res) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) rv[t][k] = rvs[t0 + t][k];
+          }
         }
         if (RES && p.res2) {  // second residual (the DPT residual units' skip input)
 #pragma unroll

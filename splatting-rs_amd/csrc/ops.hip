@@ -758,30 +758,42 @@ __global__ void __launch_bounds__(1024) ref_view_kernel(const float* xs, int V, 
     }
   }
   __syncthreads();
-  if (threadIdx.x != 0) return;
-  double sim[REF_MAX_VIEWS], nrm[REF_MAX_VIEWS], var[REF_MAX_VIEWS];
-  for (int i = 0; i < V; ++i) nrm[i] = sqrt(gram[i * V + i]);
-  for (int i = 0; i < V; ++i) {
+  // Per-view metrics, one thread per view (the reference's loops over j in the same order)
+  __shared__ double met[3][REF_MAX_VIEWS];
+  __shared__ double lohi[3][2];
+  __shared__ double bal[REF_MAX_VIEWS];
+  const int i = threadIdx.x;
+  if (i < V) {
+    const double nrm = sqrt(gram[i * V + i]);
     double s = 0.0;
     for (int j = 0; j < V; ++j)
-      if (j != i) s += gram[i * V + j] / (nrm[i] * nrm[j]);
-    sim[i] = s / (V - 1);
-    const double mean = rsum[i] / nrm[i] / dim;
-    const double sq = gram[i * V + i] / (nrm[i] * nrm[i]);
-    var[i] = (sq - dim * mean * mean) / (dim - 1);
+      if (j != i) s += gram[i * V + j] / (nrm * sqrt(gram[j * V + j]));
+    const double mean = rsum[i] / nrm / dim;
+    const double sq = gram[i * V + i] / (nrm * nrm);
+    met[0][i] = s / (V - 1);
+    met[1][i] = nrm;
+    met[2][i] = (sq - dim * mean * mean) / (dim - 1);
   }
-  double* metrics[3] = {sim, nrm, var};
-  double bal[REF_MAX_VIEWS];
-  for (int i = 0; i < V; ++i) bal[i] = 0.0;
-  for (int k = 0; k < 3; ++k) {
+  __syncthreads();
+  if (i < 3) {  // min-max range of metric i over the views
     double lo = INFINITY, hi = -INFINITY;
-    for (int i = 0; i < V; ++i) { lo = fmin(lo, metrics[k][i]); hi = fmax(hi, metrics[k][i]); }
-    for (int i = 0; i < V; ++i) bal[i] += fabs((metrics[k][i] - lo) / (hi - lo + 1e-8) - 0.5);
+    for (int v = 0; v < V; ++v) { lo = fmin(lo, met[i][v]); hi = fmax(hi, met[i][v]); }
+    lohi[i][0] = lo;
+    lohi[i][1] = hi;
   }
-  int best = 0;
-  for (int i = 1; i < V; ++i)
-    if (bal[i] < bal[best]) best = i;
-  *ref = best;
+  __syncthreads();
+  if (i < V) {
+    double b = 0.0;
+    for (int k = 0; k < 3; ++k) b += fabs((met[k][i] - lohi[k][0]) / (lohi[k][1] - lohi[k][0] + 1e-8) - 0.5);
+    bal[i] = b;
+  }
+  __syncthreads();
+  if (i == 0) {  // the first argmin
+    int best = 0;
+    for (int v = 1; v < V; ++v)
+      if (bal[v] < bal[best]) best = v;
+    *ref = best;
+  }
 }
 
 void select_reference_view(const Exec& ex, const float* xs, int V, int n, int dim, int strategy, int* ref) {
