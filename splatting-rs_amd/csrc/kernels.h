@@ -202,6 +202,9 @@ void resize_rgba8(const Exec& ex, const uint8_t* src, int W, int H, float* tmp, 
 
 // Generic elementwise helpers.
 void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, long count);
+// Row r, column c of in (row stride ldi elements) -> out (row stride ldo), converted.
+void convert_rows(const Exec& ex, int in_dt, const void* in, long ldi, int out_dt, void* out, long ldo, int rows,
+                  int cols);
 void add_rows(const Exec& ex, float* xs, int rows, int dim, const float* vec);           // xs[r] += vec
 void copy_rows_f32(const Exec& ex, float* dst, long lddst, const float* src, long ldsrc, int rows, int dim);
 // mean over groups of P rows: out[g, c] = mean_p in[g*P + p, c] (fp32 out)

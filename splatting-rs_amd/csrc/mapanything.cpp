@@ -208,8 +208,7 @@ void MaModel::forward(const float* images, int V, int H, int W, const splat_ma_o
     gemm(ex, g);
     const size_t m = ar.mark();
     void* cls_t = ar.alloc(size_t(V) * e * es);
-    for (int v = 0; v < V; ++v)
-      convert(ex, F32, xe + size_t(v) * n * e, dt_, static_cast<char*>(cls_t) + size_t(v) * e * es, e);
+    convert_rows(ex, F32, xe, long(n) * e, dt_, cls_t, e, V, e);  // the class token of each view
     GemmArgs gc = lin_args(proj_embed_, dt_, cls_t, e, V, xi, d);
     gc.out_f32 = 1;
     gc.rm_P = 1;

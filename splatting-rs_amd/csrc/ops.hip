@@ -922,6 +922,28 @@ void convert(const Exec& ex, int in_dt, const void* in, int out_dt, void* out, l
   SPLAT_HIP(hipGetLastError());
 }
 
+template <typename TI, typename TO>
+__global__ void convert_rows_kernel(const void* in, long ldi, void* out, long ldo, int rows, int cols) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)rows * cols) return;
+  const long r = id / cols, c = id - r * cols;
+  st<TO>(out, r * ldo + c, ld<TI>(in, r * ldi + c));
+}
+
+void convert_rows(const Exec& ex, int in_dt, const void* in, long ldi, int out_dt, void* out, long ldo, int rows,
+                  int cols) {
+  if (ex.dry || rows == 0 || cols == 0) return;
+  SPLAT_CHECK(in_dt_ok(in_dt) && in_dt_ok(out_dt), BAD_ARGUMENT, "convert_rows: dtype");
+  dim3 grid(cdiv((long)rows * cols, 256));
+  by_dt(in_dt, [&](auto ti) {
+    by_dt(out_dt, [&](auto to) {
+      hipLaunchKernelGGL((convert_rows_kernel<TY(ti), TY(to)>), grid, dim3(256), 0, ex.stream, in, ldi, out, ldo, rows,
+                         cols);
+    });
+  });
+  SPLAT_HIP(hipGetLastError());
+}
+
 __global__ void add_rows_kernel(float* xs, int rows, int dim, const float* vec) {
   const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (id < (long)rows * dim) xs[id] += vec[id % dim];
