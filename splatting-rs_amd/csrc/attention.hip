@@ -775,6 +775,7 @@ __global__ void __launch_bounds__(256, 2) attn_f32_kernel(const AttnArgs p, floa
     const char* kb = smem + B * TB;
     const char* vb = smem + (2 + B) * TB;
     f32x16 s = {};
+    __builtin_amdgcn_s_setprio(1);  // matrix-core sections first among the SIMD's waves (as above)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {  // channels 4 i .. 4 i + 3 (+ 32 g)
       const float4 kf = *reinterpret_cast<const float4*>(kb + l32 * 256 + (((8 * g + i) ^ ks) * 16));
@@ -783,6 +784,7 @@ __global__ void __launch_bounds__(256, 2) attn_f32_kernel(const AttnArgs p, floa
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[4 * i + 2], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[4 * i + 3], s, 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
     if constexpr (masked) {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
@@ -810,6 +812,7 @@ __global__ void __launch_bounds__(256, 2) attn_f32_kernel(const AttnArgs p, floa
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) lsum += s[r];
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
       const int col = dt * 32 + l32;  // head channel of this lane's V reads
@@ -820,6 +823,7 @@ __global__ void __launch_bounds__(256, 2) attn_f32_kernel(const AttnArgs p, floa
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf, s[r], o[dt], 0, 0, 0);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   const int ntiles = (L + 31) / 32;
