@@ -945,7 +945,11 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnArgs p) {
 // blocks, plus 2% per slice for the partials and the merge, over S = 1..4 with at least 8 key
 // tiles a slice (C4 global 196 -> 172 us with 3 slices, C5 global 2207 -> 2092 us with 3,
 // DA3-Small C2 global 122 -> 85 us with 4).
-static int attn_splits(long blocks, int ntiles) {
+static int attn_splits(long blocks, int ntiles, bool qt2) {
+  // Unsplit when the grid is resident at once with at least two blocks a CU (four QT=1 or two
+  // QT=2 blocks fit a CU): the merge costs more than the balance it buys (C4 global, 588 blocks:
+  // 146 us unsplit against 152 us in 3 slices, measured with the matrix-core wave priorities).
+  if (blocks >= 2 * 256 && blocks <= (qt2 ? 2 : 4) * 256) return 1;
   int best = 1;
   double bc = 1e30;
   for (int S = 1; S <= 4; ++S) {
@@ -1010,7 +1014,7 @@ void attention(const Exec& ex, const AttnArgs& a) {
   const long blocks = qt2 ? blocks2 : long(cdiv(a.L, 128)) * a.heads * a.seqs;
   // the fp32 kernel's 32-key tiles: slices of at least 4 tiles, about two blocks per CU
   const int ntiles = f32_fast ? cdiv(a.L, 32) : cdiv(a.L, 64);
-  const int S = bf_fast    ? (a.L >= 4096 ? attn_splits(blocks, ntiles) : 1)
+  const int S = bf_fast    ? (a.L >= 4096 ? attn_splits(blocks, ntiles, qt2) : 1)
                 : f32_fast ? int(std::min<long>(std::min<long>(8, std::max(1, ntiles / 4)), std::max<long>(1, cdiv(512, gblocks))))
                            : int(std::min<long>(std::min<long>(8, ntiles / 2), std::max<long>(1, cdiv(512, gblocks))));
   AttnArgs b = a;
