@@ -1005,13 +1005,24 @@ void attention(const Exec& ex, const AttnArgs& a) {
   // has about two blocks per CU (DA3-Small C1: 66 blocks -> 7 slices).
   const long gblocks = long(cdiv(a.L, ATTN_WAVES * 32)) * a.heads * a.seqs;
   // 4 waves x 32 or 64 queries. Two query sub-tiles per wave (QT = 2) halve the K/V reads per
-  // query and win once their grid gives each CU about two blocks (C5 global 2.46 vs 2.85 ms);
-  // below that the doubled block size leaves CUs idle (C4 global, 300 such blocks: 261 vs
-  // 242 us; C4 info-sharing per-view, 360: +8 us a launch; C4 encoder per-view, 480: 1.5% of the
-  // attention time).
+  // query; four QT=1 or two QT=2 blocks fit a CU. Unsplit launches (L < 4096) take QT = 2 when
+  // the most work any CU gets, in QT=1 block units (ceil(blocks / CUs) x QT), is smaller with it,
+  // or equal with every CU given a QT=2 block (per shape, with the matrix-core wave priorities:
+  // C4 encoder per-view 480 blocks 38.9 vs 40.9 us; C4 info-sharing per-view 360 blocks, C5
+  // per-view 1920 and 1440 blocks and C2 per-view 144 blocks all faster on QT=1). Longer
+  // sequences: QT = 2 from 500 blocks (C5 global 1.61 vs 1.72 ms; C4 global, 300 such blocks, 156
+  // vs 139 us), and when the QT=1 grid has fewer than two blocks a CU and slices anyway (C2 global
+  // 66.8 vs 74.6 us).
+  const long blocks1 = long(cdiv(a.L, 128)) * a.heads * a.seqs;
   const long blocks2 = long(cdiv(a.L, 256)) * a.heads * a.seqs;
-  const bool qt2 = blocks2 >= 500;
-  const long blocks = qt2 ? blocks2 : long(cdiv(a.L, 128)) * a.heads * a.seqs;
+  bool qt2;
+  if (a.L >= 4096) {
+    qt2 = blocks2 >= 500 || blocks1 < 512;
+  } else {
+    const long u1 = (blocks1 + 255) / 256, u2 = 2 * ((blocks2 + 255) / 256);
+    qt2 = u2 < u1 || (u2 == u1 && blocks2 >= 256);
+  }
+  const long blocks = qt2 ? blocks2 : blocks1;
   // the fp32 kernel's 32-key tiles: slices of at least 4 tiles, about two blocks per CU
   const int ntiles = f32_fast ? cdiv(a.L, 32) : cdiv(a.L, 64);
   const int S = bf_fast    ? (a.L >= 4096 ? attn_splits(blocks, ntiles, qt2) : 1)

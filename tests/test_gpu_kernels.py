@@ -122,11 +122,12 @@ ATTN_CASES = [
     (3, 130, 1),
     (6, 973, 6),
     (1, 1297, 6),    # DA3-Small C1 (fp32: 7 key slices of 32-key tiles)
-    (1, 5838, 6),    # DA3-Small C2 global: 276 blocks in 4 key slices, ragged last tile
+    (1, 5838, 6),    # DA3-Small C2 global: 138 blocks of 256 queries in 3 key slices, ragged last tile
     (2, 1037, 16),
-    (6, 1037, 16),   # 480 blocks: one query sub-tile per wave (the C4 encoder's per-view shape)
-    (7, 1037, 16),   # 560 blocks of 256 queries: two query sub-tiles per wave, ragged last key tile
-    (9, 1100, 12),   # 540 blocks: the same with another ragged end
+    (6, 1037, 16),   # the C4 encoder's per-view shape: 480 blocks of 256 queries, two query sub-tiles per wave
+    (6, 1100, 16),   # the same with another ragged last key tile
+    (7, 1037, 16),   # 1008 blocks of 128 queries: one query sub-tile per wave, ragged last key tile
+    (9, 1100, 12),   # 972 blocks: the same with another ragged end
     # long sequences: key slices merged by a second kernel where the grid leaves block slots idle
     (1, 6223, 12),   # the MapAnything C4 global block (588 blocks, resident at once: unsplit, ragged last tile)
     (1, 4096, 33),   # two query sub-tiles per wave with slices, no ragged tile
