@@ -281,6 +281,19 @@ def main():
     wall = time.perf_counter() - wall0
     ms = e0.elapsed_time(e1) / args.steps
     log(f"{cfg.key}: {ms:.3f} ms/forward (events), wall {1e3 * wall / args.steps:.3f} ms/step")
+    # after the timed region: forwards timed one by one (an event pair around each) for the
+    # median and the 90th percentile
+    pairs = []
+    for _ in range(min(args.steps, 50)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        step()
+        b.record(stream)
+        pairs.append((a, b))
+    ctx.synchronize()
+    each = sorted(a.elapsed_time(b) for a, b in pairs)
+    ms_median, ms_p90 = each[len(each) // 2], each[min(len(each) - 1, (9 * len(each)) // 10)]
+    log(f"{cfg.key}: median {ms_median:.3f} ms, p90 {ms_p90:.3f} ms over {len(each)} single forwards")
 
     # one profiled forward: per-kernel-class durations from HIP events on the library stream
     ctx.profile_begin()
@@ -349,6 +362,8 @@ def main():
                    "width": cfg.width, "global_tokens": tokens, "graphs": not args.no_graphs,
                    "parallelism": "none (1 GPU)"},
         "ms_per_forward": ms,
+        "ms_per_forward_median": ms_median,
+        "ms_per_forward_p90": ms_p90,
         "forward_tflop": mfma_flops / 1e12,
         "mfma_util_forward": mfma_flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype],
         "mfma_util_mfma_kernels": (mfma_flops / (mfma_ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype]) if mfma_ms else None,
