@@ -1194,7 +1194,7 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
 
 // Split-K reduction: out = epilogue(sum over slices of the fp32 partials), 8 columns a thread.
 template <typename T>
-__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p, int S) {
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p, int S, int stats) {
   const long runs = (p.N + 7) / 8;
   const long id = long(blockIdx.x) * 256 + threadIdx.x;
   if (id >= long(p.M) * runs) return;
@@ -1210,6 +1210,27 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p, in
     for (int k = 0; k < 8; ++k) v[k] += w[k];
   }
   epi8<T>(p, v, m, n, p.epi_vec && n + 8 <= p.N);
+  if (stats) {
+    // A producer's row statistics (and copy) of the stored rows: a group of ln_group columns is
+    // ln_group / 8 consecutive lanes (N a multiple of the group, so groups are lane-aligned and
+    // whole), summed by DPP; the group's first lane writes the (sum, sum of squares) pair.
+    float sm = 0.f, sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      sm += v[k];
+      sq = fmaf(v[k], v[k], sq);
+    }
+    if (p.ln_group == 64) {
+      sm = group_sum<8>(sm);
+      sq = group_sum<8>(sq);
+    } else {
+      sm = group_sum<16>(sm);
+      sq = group_sum<16>(sq);
+    }
+    if ((n % p.ln_group) == 0)
+      *reinterpret_cast<float2*>(p.ln_out + (m * (p.N / p.ln_group) + n / p.ln_group) * 2) = make_float2(sm, sq);
+    if (p.ln_copy) store8_to<T>(p.ln_copy, false, v, m * p.ldc + n);
+  }
 }
 
 constexpr int GEMM_CUS = 256;  // MI355X compute units: one "round" of resident blocks per CU slot
@@ -1277,12 +1298,16 @@ static bool launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   }
 #undef SPLAT_GO
   SPLAT_HIP(hipGetLastError());
+  // the reduce of a split producer emits its row statistics too (whole 8-column runs, plain rows)
+  const bool rstats = S > 1 && a.ln_out && a.epi_vec && !a.rm_P && a.store == STORE_ROWS &&
+                      (a.ln_group == 64 || a.ln_group == 128) && a.N % a.ln_group == 0;
   if (S > 1) {
     const long work = long(a.M) * ((a.N + 7) / 8);
-    hipLaunchKernelGGL(splitk_reduce_kernel<T>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b, S);
+    hipLaunchKernelGGL(splitk_reduce_kernel<T>, dim3(unsigned((work + 255) / 256)), dim3(256), 0, ex.stream, b, S,
+                       int(rstats));
     SPLAT_HIP(hipGetLastError());
   }
-  return epi == EPI_RESLN;
+  return epi == EPI_RESLN || rstats;
 }
 
 // Tile configurations of the bf16 path: block tile, and how many blocks share a CU.

@@ -488,8 +488,8 @@ LN_PRODUCER_CASES = [
     (6223, 768, 768, 64),     # info proj: 192x128 tiles (32-column waves: sums meet in LDS)
     (6223, 768, 3072, 64),    # info fc2
     (5838, 384, 1536, 64),    # DA3-Small C2 fc2: 128x128 tiles
-    (1297, 384, 1536, 64),    # DA3-Small C1 fc2: split-K, statistics from the ln_stats kernel
-    (1297, 1536, 1536, 128),  # split-K, 128-column groups
+    (1297, 384, 1536, 64),    # DA3-Small C1 fc2: split-K, statistics from the reduce kernel
+    (1297, 1536, 1536, 128),  # split-K, 128-column groups (16-lane sums in the reduce kernel)
     (1400, 1536, 1536, 128),  # reference-dims MapAnything proj (128-column groups)
     (6222, 4096, 1024, 128),  # 400 tiles of 256x256 (1.56 rounds), 32 groups a row
     (200, 128, 64, 64),       # one row tile, ragged
