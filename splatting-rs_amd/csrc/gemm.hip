@@ -454,7 +454,6 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, f32x16 (&acc)[TM][TN
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
           const int rr = rsub + (t0 + t) * (64 / RUNS);
-          const long m = wrow0 + i * 32 + rr;
           read8(slab + rr * LD + cc, v[t]);
           if (RES && p.res) {
 #pragma unroll
