@@ -211,7 +211,7 @@ inline int cdiv(long a, long b) { return int((a + b - 1) / b); }
 // b+16, ... to one of the 8 XCDs (each with its own L2), so XCD x gets the contiguous range of
 // logical ids starting at x*(nblk/8) (the first nblk%8 XCDs one id more). Neighbouring ids
 // then share operands in one L2. A bijection of [0, nblk).
-__device__ inline int xcd_contiguous(int b, int nblk) {
+__host__ __device__ inline int xcd_contiguous(int b, int nblk) {
   const int x = b & 7, q8 = nblk >> 3, r8 = nblk & 7;
   return (x < r8 ? x * (q8 + 1) : r8 * (q8 + 1) + (x - r8) * q8) + (b >> 3);
 }

@@ -881,19 +881,18 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   const int wm = wave / WN, wn = wave % WN;
   const int g = lane >> 5, l32 = lane & 31;
 
-  // Tile order, walked in groups of 8 tile rows so that neighbouring tiles share A and W
-  // panels. Blocks b, b+8, ... land on one XCD (round-robin dispatch): when the tile count is a
-  // multiple of 8 each XCD takes a contiguous run of tiles (8192^3: 1.30 vs 1.01 PFLOP/s
-  // dealt round-robin); otherwise the round-robin deal, which keeps one tile row per XCD and
-  // measured the same time and less HBM traffic than contiguous runs on the network's shapes.
+  // Tile order, walked in groups of p.tgroup tile rows so that neighbouring tiles share A and W
+  // panels. Blocks b, b+8, ... land on one XCD (round-robin dispatch): with p.tcontig each XCD
+  // takes a contiguous run of tiles, else the round-robin deal (the launcher's choice).
   const int nblk = tiles_m * tiles_n;
   // split-K slices (EPI_PART): block b covers tile b % nblk over k-tiles [kt0, kt0 + nk)
   const int split = EPI == EPI_PART ? int(blockIdx.x) / nblk : 0;
   const int b0 = int(blockIdx.x) - split * nblk;
-  const int bid = (EPI != EPI_PART && (nblk & 7) == 0) ? xcd_contiguous(b0, nblk) : b0;
-  const int per_group = 8 * tiles_n;
-  const int first_m = (bid / per_group) * 8;
-  const int gsize = min(tiles_m - first_m, 8);
+  const int bid = (EPI != EPI_PART && p.tcontig) ? xcd_contiguous(b0, nblk) : b0;
+  const int tg = p.tgroup;
+  const int per_group = tg * tiles_n;
+  const int first_m = (bid / per_group) * tg;
+  const int gsize = min(tiles_m - first_m, tg);
   const int tm = first_m + (bid % per_group) % gsize;
   const int tn = (bid % per_group) / gsize;
   const long m0 = long(tm) * BM, n0 = long(tn) * BN;
@@ -1234,6 +1233,53 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p, in
 
 constexpr int GEMM_CUS = 256;  // MI355X compute units: one "round" of resident blocks per CU slot
 
+// XCD-aware tile map of a row GEMM. The 8 XCDs have an L2 each, so a launch fetches into each
+// L2 the A panels of the tile rows and the W panels of the tile columns that the XCD's blocks
+// touch (each panel BM or BN rows by K). Among tile-group heights 8, 1 and ceil(tm / r) for
+// r = 2, 4, 8, each with contiguous runs and with the round-robin deal, take the map whose
+// blocks touch the fewest panel rows (BM per tile row plus BN per tile column, summed over the
+// XCDs); ties keep 8-row groups and the deal the tile count gave before. Encoder qkv at C4
+// (20 x 12 tiles of 320x256): 67.9 -> 51.4 MB of panels (groups of 5 rows: each XCD a 5 x 6
+// block); fc2 (25 x 8 tiles of 256x128, K = 4096): 197 -> 134 MB. Cached per shape.
+struct XcdTileMap { int tm, tn, bm, bn, group, contig; };
+static void xcd_tile_map(GemmArgs& b, int tm, int tn, int bm, int bn) {
+  const int nblk = tm * tn;
+  if (nblk > 4096) return;
+  static thread_local std::vector<XcdTileMap> cache;
+  for (const XcdTileMap& c : cache)
+    if (c.tm == tm && c.tn == tn && c.bm == bm && c.bn == bn) {
+      b.tgroup = c.group;
+      b.tcontig = c.contig;
+      return;
+    }
+  std::vector<char> rows(size_t(8) * tm), cols(size_t(8) * tn);
+  auto cost = [&](int g, bool contig) {
+    std::fill(rows.begin(), rows.end(), 0);
+    std::fill(cols.begin(), cols.end(), 0);
+    long c = 0;
+    for (int blk = 0; blk < nblk; ++blk) {
+      const int x = blk & 7, bid = contig ? xcd_contiguous(blk, nblk) : blk;
+      const int per_group = g * tn, first = (bid / per_group) * g, gs = std::min(tm - first, g);
+      const int r = first + (bid % per_group) % gs, q = (bid % per_group) / gs;
+      if (!rows[size_t(x) * tm + r]) { rows[size_t(x) * tm + r] = 1; c += bm; }
+      if (!cols[size_t(x) * tn + q]) { cols[size_t(x) * tn + q] = 1; c += bn; }
+    }
+    return c;
+  };
+  int best_g = b.tgroup, best_contig = b.tcontig;
+  long best = cost(best_g, best_contig);
+  const int gs[] = {8, 1, cdiv(tm, 2), cdiv(tm, 4), cdiv(tm, 8)};
+  for (int g : gs)
+    for (int contig = 1; contig >= 0; --contig) {
+      if (g < 1) continue;
+      const long c = cost(g, contig);
+      if (c < best) { best = c; best_g = g; best_contig = contig; }
+    }
+  b.tgroup = best_g;
+  b.tcontig = best_contig;
+  cache.push_back({tm, tn, bm, bn, best_g, best_contig});
+}
+
 // TAP_ONLY: an instantiation that serves per-tap convolutions only (the 32-element k-tiles for
 // maps whose Cin is a multiple of 32 but not of 64).
 // Returns whether the launch wrote the row statistics (and copy) a producer (ln_out) asks for.
@@ -1247,6 +1293,9 @@ static bool launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   SPLAT_CHECK(!a.ln_in || (epi == EPI_LN && a.amode == A_ROWS && !TAP_ONLY), BAD_ARGUMENT,
               "gemm: a folded LayerNorm needs plain rows, a vectorisable epilogue and no split-K");
   GemmArgs b = a;
+  b.tgroup = 8;
+  b.tcontig = (tm * tn) % 8 == 0;
+  if (a.amode == A_ROWS && S == 1) xcd_tile_map(b, tm, tn, BM, BN);
   if (S > 1) {
     b.part = static_cast<float*>(ex.ws->ptr);
     b.ldp = (a.N + 7) / 8 * 8;

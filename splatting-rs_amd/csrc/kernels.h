@@ -44,6 +44,9 @@ struct GemmArgs {
   int store = STORE_ROWS;
   int ct_s = 1, ct_R = 0, ct_C = 0, ct_Cout = 0;
   int epi_vec = 0;  // set by gemm(): the epilogue may use 16-byte vector accesses
+  // Set by the launcher: tiles are walked in groups of tgroup tile rows (column by column inside
+  // a group); with tcontig each XCD takes a contiguous run of that order, else the round-robin deal.
+  int tgroup = 8, tcontig = 0;
   // Set by gemm() for a split-K launch: fp32 partial sums [splits][M][ldp], kper k-tiles each.
   float* part = nullptr; long ldp = 0; int kper = 0;
   // MapAnything output head fused into the epilogue (bf16 convolution with N = 128, act ReLU):
