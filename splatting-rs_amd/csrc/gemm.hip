@@ -1240,11 +1240,14 @@ constexpr int GEMM_CUS = 256;  // MI355X compute units: one "round" of resident 
 // blocks touch the fewest panel rows (BM per tile row plus BN per tile column, summed over the
 // XCDs); ties keep 8-row groups and the deal the tile count gave before. Encoder qkv at C4
 // (20 x 12 tiles of 320x256): 67.9 -> 51.4 MB of panels (groups of 5 rows: each XCD a 5 x 6
-// block); fc2 (25 x 8 tiles of 256x128, K = 4096): 197 -> 134 MB. Cached per shape.
+// block); fc2 (25 x 8 tiles of 256x128, K = 4096): 197 -> 134 MB. Cached per shape. Only for
+// launches of at most two rounds, whose blocks run nearly all at once: over more rounds the
+// order in time matters more than the union of panels (8192^3, four rounds: contiguous runs
+// 1.30 PFLOP/s, the round-robin deal 1.01), so those keep the default.
 struct XcdTileMap { int tm, tn, bm, bn, group, contig; };
 static void xcd_tile_map(GemmArgs& b, int tm, int tn, int bm, int bn) {
   const int nblk = tm * tn;
-  if (nblk > 4096) return;
+  if (nblk > 2 * GEMM_CUS) return;
   static thread_local std::vector<XcdTileMap> cache;
   for (const XcdTileMap& c : cache)
     if (c.tm == tm && c.tn == tn && c.bm == bm && c.bn == bn) {
