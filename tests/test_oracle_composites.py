@@ -604,3 +604,136 @@ def test_mapanything_patches_are_fusion_normed_and_the_class_token_is_raw():
     assert len(info_taps) == len(want) == spec.info_depth
     assert torch.allclose(info_taps[-1], want[-1], atol=1e-10)
     assert not torch.allclose(wrong[-1], want[-1], atol=1e-6)
+
+
+# --- token assembly and forward wiring: mapanything-rs/src/{dinov2.rs:129-145, model.rs:86-144},
+# depthanything3-rs/src/backbone.rs:140-163 ---------------------------------------------------
+
+def patch_embed(images, w, b):
+    """Conv2d(3, d, 14, stride 14) from its definition: each 14x14 patch flattened in (channel,
+    row, column) order against the [d, 3, 14, 14] kernel, plus the bias."""
+    V, ch, H, W = images.shape
+    R, Cc = H // 14, W // 14
+    cols = images.reshape(V, ch, R, 14, Cc, 14).permute(0, 2, 4, 1, 3, 5).reshape(V, R * Cc, ch * 196)
+    return cols @ w.reshape(w.shape[0], -1).T + b
+
+
+def _embedded_tokens(p, prefix, images):
+    """cat(cls, patch_embed(x)) + pos over all 1 + P slots (class slot = cls + pos_embed[0, 0])."""
+    V, _, H, W = images.shape
+    R, Cc = H // 14, W // 14
+    pos = C.positional_embedding(p[prefix + ".pos_embed"], R, Cc)[0].to(D64)
+    assert torch.equal(pos[0], p[prefix + ".pos_embed"][0, 0].float().to(D64))  # class slot not resized
+    pe = patch_embed(images, p[prefix + ".patch_embed.proj.weight"], p[prefix + ".patch_embed.proj.bias"])
+    cls = p[prefix + ".cls_token"].reshape(1, 1, -1).expand(V, 1, pe.shape[-1])
+    return torch.cat([cls, pe], 1) + pos
+
+
+def test_mapanything_encoder_token_assembly_closed_form():
+    """mapanything-rs/src/dinov2.rs:129-145 with LayerScale 0 (every block the identity): the
+    encoder returns cat(cls, patch_embed(x)) + pos over all 1 + P slots. Fails if the class token
+    is appended last, if the positional embedding skips the class slot, or if a final norm is
+    applied (the reference's encoder has none)."""
+    spec = specs.MA_SPECS["tiny"]
+    w = synth.generate(synth.ma_shapes(spec), seed=21, layer_scale=0.0)
+    p = C.to_torch(w, D64)
+    p["encoder.model.cls_token"] = p["encoder.model.cls_token"] * 50      # well away from pos and the patches
+    images = torch.from_numpy(synth.uniform_images(2, 28, 42, seed=4)).to(D64)
+    got = OM.encoder_forward(p, spec, images)
+    want = _embedded_tokens(p, "encoder.model", images)
+    assert got.shape == (2, 7, spec.enc_dim)
+    assert torch.allclose(got, want, atol=1e-12)
+    # forward() hands the same tokens on (encoder_only): no norm between encoder and caller
+    out = OM.forward(p, spec, images, dtype=D64, encoder_only=True)
+    assert torch.allclose(out["encoder_tokens"].to(D64), want, atol=1e-5)
+
+
+def _mean_block_0(p, prefix, d):
+    """Block 0 adds each sequence's mean of LN(x) over its tokens (q = k = 0: uniform attention;
+    v = LN1(x) with norm1 weight 1 / bias 0; proj I; LayerScale 1, feed-forward LayerScale 0)."""
+    n = f"{prefix}.blocks.0"
+    p[n + ".norm1.weight"], p[n + ".norm1.bias"] = torch.ones(d, dtype=D64), torch.zeros(d, dtype=D64)
+    qkv = torch.zeros(3 * d, d, dtype=D64)
+    qkv[2 * d:] = torch.eye(d, dtype=D64)
+    p[n + ".attn.qkv.weight"], p[n + ".attn.qkv.bias"] = qkv, torch.zeros(3 * d, dtype=D64)
+    p[n + ".attn.proj.weight"], p[n + ".attn.proj.bias"] = torch.eye(d, dtype=D64), torch.zeros(d, dtype=D64)
+    p[n + ".ls1.gamma"], p[n + ".ls2.gamma"] = torch.ones(d, dtype=D64), torch.zeros(d, dtype=D64)
+
+
+def test_da3_class_slot_carries_pos0_into_the_reference_view_choice():
+    """depthanything3-rs/src/backbone.rs:140-163: the class slot starts as cls + pos_embed[0, 0]
+    (the positional embedding covers all 1 + P slots), and the saddle-balanced selection before
+    block alt_start - 1 reads it. Block 0 adds each view's mean of LN(x) over its n tokens and
+    every other block is the identity (LayerScale 0), so the selection sees cls + pos[0] +
+    mean_t LN(x_t), computed here from first principles; the selection itself is pinned by
+    reference_view.rs's KATs (test_oracle.py). The weights are chosen so that dropping pos[0]
+    from the class slot selects another view (asserted below), besides changing the tap."""
+    spec = specs.DA3_VARIANTS["small"]
+    d = spec.dim
+    b = "model.backbone.pretrained"
+    w = synth.generate(synth.da3_shapes(spec), seed=23, layer_scale=0.0)
+    p = C.to_torch(w, D64)
+    g = torch.Generator().manual_seed(4)
+    pos = p[b + ".pos_embed"].clone()
+    pos[0, 0] = rng_t(g, d, scale=1.0)
+    p[b + ".pos_embed"] = pos
+    _mean_block_0(p, b, d)
+    V = 5
+    images = torch.from_numpy(synth.procedural_images(V, 28, 42, seed=24)).to(D64)
+    taps = []
+    layers, cam, ref = OD.backbone_forward(p, spec, images, OD.REF_SADDLE, taps=taps)
+    x = _embedded_tokens(p, b, images)
+    cls_after = x[:, 0] + ln(x, 1e-6).mean(1)
+    assert torch.allclose(taps[0][:, 0], cls_after, atol=1e-12)
+    assert torch.allclose(taps[spec.alt_start - 2][:, 0], cls_after, atol=1e-12)
+    want = OD.select_reference_view(cls_after.float().numpy(), OD.REF_SADDLE)
+    assert ref == want == 3
+    # the test discriminates: without pos[0] on the class slot the choice moves
+    x_slip = x.clone()
+    x_slip[:, 0] -= pos[0, 0].float().to(D64)
+    slip = OD.select_reference_view((x_slip[:, 0] + ln(x_slip, 1e-6).mean(1)).float().numpy(), OD.REF_SADDLE)
+    assert slip != want, (slip, want)
+
+
+def test_mapanything_forward_wiring():
+    """mapanything-rs/src/model.rs:86-144 with a closed-form encoder (LayerScale 0) and info blocks
+    that each add a constant c_i (proj bias, LayerScale 1 / 0): the dense head's hooks are
+    [LN_fusion(patches), LN(x + sum c) after each hook block], hook 0 being the fusion-normed
+    encoder patches (model.rs:106, not the raw tokens); the pose head reads the normed last hook
+    (model.rs:132); the scale head reads the normed scale token of the last hook; translation is
+    fc_t times the scale (model.rs:140). The DPT, pose and scale heads are pinned by their own
+    closed forms above and are called here on inputs computed from first principles."""
+    spec = specs.MA_SPECS["tiny"]
+    g = torch.Generator().manual_seed(25)
+    w = synth.generate(synth.ma_shapes(spec), seed=25, layer_scale=0.0)
+    p = C.to_torch(w, D64)
+    ip, cs = _info_params(spec, g, "const")
+    p.update(ip)
+    p["scale_head.output_proj.bias"] = p["scale_head.output_proj.bias"] + 0.7    # scale well away from 1
+    V, R, Cc = 3, 2, 3
+    images = torch.from_numpy(synth.procedural_images(V, 28, 42, seed=26)).to(D64)
+    out = OM.forward(p, spec, images, dtype=D64)
+
+    tokens = _embedded_tokens(p, "encoder.model", images)
+    fused = ln(tokens[:, 1:], 1e-6) * p["fusion_norm_layer.weight"] + p["fusion_norm_layer.bias"]
+    nw, nb = p["info_sharing.norm.weight"], p["info_sharing.norm.bias"]
+    vp = p["info_sharing.view_pos_table"][0]
+    hooks = [fused]
+    for hk in spec.hooks:
+        x = fused + sum(cs[: hk + 1])
+        x[0] = x[0] + vp
+        hooks.append(ln(x, 1e-6) * nw + nb)
+    s = p["scale_token"] + sum(cs[j] for j in range(spec.hooks[2] + 1) if j % 2 == 0)
+    scale = OM.scale_head(p, (ln(s, 1e-6) * nw + nb)[None])[0]
+    raw = OM.dpt_forward(p, spec, hooks, R, Cc)
+    spatial = hooks[3].transpose(1, 2).reshape(V, spec.info_dim, R, Cc)
+    trans, quat = OM.pose_head(p, spatial)
+    assert abs(float(scale) - 1.0) > 0.3
+    assert abs(out["scale"] - float(scale)) < 1e-12
+    assert torch.allclose(out["raw"].to(D64), raw, atol=1e-10)
+    assert torch.allclose(out["quaternion"].to(D64), quat, atol=1e-6)
+    assert torch.allclose(out["translation_raw"].to(D64), trans, atol=1e-6)
+    assert torch.allclose(out["translation"].to(D64), trans * scale, atol=1e-6)
+    pts, conf, mask = OM.dense_output(raw, scale)
+    assert torch.allclose(out["points"].to(D64), pts, atol=1e-5)
+    assert torch.equal(out["mask"], mask)
