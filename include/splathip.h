@@ -150,7 +150,9 @@ int splat_set_branch_taps(splat_ctx* ctx, splat_branch_tap_fn fn, void* user);
 /* mapanything-rs/src/image_input.rs:195-216 (to_model_input, used by both crates' preprocess):
  * host RGBA u8 [V, H, W, 4] (already resized and cropped) -> device images [V, 3, H, W] f32,
  * ImageNet-normalised, and device foreground [V, H, W] u8 = alpha >= 128 (NULL: skipped).
- * Uploads 4 bytes per pixel instead of 12; enqueued on splat_stream. */
+ * Uploads 4 bytes per pixel instead of 12. A view without a pixel of alpha >= 128 is the
+ * reference's error (image_input.rs:197 "fully transparent after cropping"): SPLAT_BAD_ARGUMENT
+ * naming the view, as for the two model_inputs entry points below. Synchronises splat_stream. */
 int splat_to_model_input(splat_ctx* ctx, const uint8_t* rgba, int V, int H, int W, float* images, uint8_t* foreground);
 
 /* --- image preprocessing: the crates' load_images from decoded RGBA onwards, on the device ---- */

@@ -54,10 +54,13 @@ int splat_kernel_attention(splat_ctx* ctx, int dtype, const void* qkv, void* out
  * loops, harnesses that forbid hipMalloc). Same kernels and key-slice plan; the fp32 partials
  * of a key-sliced launch (long sequences) live in a statically allocated scratch of 64 MiB per
  * GPU (ATTN_SCRATCH_BYTES, held by every GPU the library runs on until the process ends)
- * instead of the context's workspace. A launch whose partials need more than that returns
- * SPLAT_BAD_ARGUMENT (e.g. 24889 tokens x 12 heads needs 236 MB; 6223 x 12 needs 59 MB). Every
- * call on one GPU shares that scratch, which keeps the last call's contents: calls that
- * overlap on one GPU (other contexts or streams) race. Profiling records are not taken. */
+ * instead of the context's workspace. A launch whose partials would need more than that (e.g.
+ * 24889 tokens x 12 heads: 236 MB; 6223 x 12 needs 59 MB and fits) runs as one key slice, with
+ * no partials: the same softmax, not bit-identical to the sliced result. Every call on one GPU
+ * shares that scratch, which keeps the last call's contents. Eager calls are ordered by the
+ * library (each waits, on its stream, for the previous call's kernels on any context of that GPU,
+ * through an event; no allocation); calls under stream capture are not, so captured graphs that
+ * replay concurrently on one GPU race. Profiling records are not taken. */
 int splat_kernel_attention_noalloc(splat_ctx* ctx, int dtype, const void* qkv, void* out, int S, int L, int heads);
 
 /* Convolution (zero padding ks/2) on NHWC maps as an implicit GEMM:

@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <functional>
 #include <mutex>
 #include <type_traits>
 
@@ -28,6 +29,11 @@ static __device__ __align__(256) char scratch[ATTN_SCRATCH_BYTES];
 namespace {
 std::mutex g_scratch_mu;
 void* g_scratch_addr[ATTN_SCRATCH_DEVICES] = {};
+// Per device: the event recorded after the last eager launch that used the scratch, and the lock
+// that orders the wait / launch / record sequences of concurrent callers.
+hipEvent_t g_scratch_done[ATTN_SCRATCH_DEVICES] = {};
+bool g_scratch_recorded[ATTN_SCRATCH_DEVICES] = {};
+std::mutex g_scratch_order[ATTN_SCRATCH_DEVICES];
 }  // namespace
 
 void* attention_scratch(int device) {
@@ -40,9 +46,26 @@ void* attention_scratch(int device) {
     void* p = nullptr;
     SPLAT_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     SPLAT_CHECK(p != nullptr, HIP_ERROR, "attention scratch: no device address");
+    SPLAT_HIP(hipEventCreateWithFlags(&g_scratch_done[device], hipEventDisableTiming));
     g_scratch_addr[device] = p;
   }
   return g_scratch_addr[device];
+}
+
+void attention_scratch_ordered(int device, hipStream_t stream, const std::function<void()>& launch) {
+  SPLAT_CHECK(device >= 0 && device < ATTN_SCRATCH_DEVICES && g_scratch_done[device], BAD_ARGUMENT,
+              "attention scratch: not set up on this device");
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  SPLAT_HIP(hipStreamIsCapturing(stream, &cap));
+  if (cap != hipStreamCaptureStatusNone) {  // a captured launch: the caller's graph orders it
+    launch();
+    return;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_order[device]);
+  if (g_scratch_recorded[device]) SPLAT_HIP(hipStreamWaitEvent(stream, g_scratch_done[device], 0));
+  launch();
+  SPLAT_HIP(hipEventRecord(g_scratch_done[device], stream));
+  g_scratch_recorded[device] = true;
 }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));

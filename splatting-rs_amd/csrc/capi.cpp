@@ -441,8 +441,9 @@ int splat_kernel_attention_noalloc(splat_ctx* ctx, int dtype, const void* qkv, v
     Context* c = C(ctx);
     const AttnArgs a = attention_args(dtype, qkv, out, S, L, heads);
     // the same kernels and key-slice plan as splat_kernel_attention, with the partials in this
-    // device's static scratch instead of the context's workspace; no profiling records (their
-    // events are created per launch)
+    // device's static scratch instead of the context's workspace; a launch whose partials would
+    // not fit runs as one key slice (no partials), as attention() does on an unsized workspace.
+    // No profiling records (their events are created per launch).
     SPLAT_CHECK(c->attn_scratch != nullptr, HIP_ERROR, "attention scratch: not set up");
     Workspace ws;
     ws.ptr = c->attn_scratch;
@@ -450,13 +451,7 @@ int splat_kernel_attention_noalloc(splat_ctx* ctx, int dtype, const void* qkv, v
     Exec e = c->ex;
     e.ws = &ws;
     e.prof = nullptr;
-    Exec dry = e;
-    dry.dry = true;
-    attention(dry, a);  // sizes the partials of the launch's key slices in ws.need
-    SPLAT_CHECK(ws.need <= ws.cap, BAD_ARGUMENT,
-                "attention: the key-slice partials of this launch need " + std::to_string(ws.need) +
-                    " bytes of scratch; the allocation-free entry point has " + std::to_string(ws.cap));
-    attention(e, a);
+    attention_scratch_ordered(c->device, e.stream, [&] { attention(e, a); });
   });
 }
 
@@ -586,7 +581,7 @@ int splat_to_model_input(splat_ctx* ctx, const uint8_t* rgba, int V, int H, int 
     const size_t px = size_t(V) * H * W;
     uint8_t* d = static_cast<uint8_t*>(staging(c, 26, px * 4));
     SPLAT_HIP(hipMemcpyAsync(d, rgba, px * 4, hipMemcpyHostToDevice, c->stream));
-    to_model_input(c->ex, d, V, H, W, images, foreground);
+    model_input(*c, d, V, H, W, images, foreground);
   });
 }
 

@@ -8,6 +8,8 @@
 #include <string>
 #include <vector>
 
+#include "errors.h"
+
 namespace splat {
 
 using bf16 = uint16_t;  // bfloat16 storage
@@ -15,28 +17,13 @@ struct f16 {            // IEEE binary16 storage (the reference's --precision f1
   uint16_t bits;
 };
 
-// --- errors -------------------------------------------------------------------------------
-
-enum Status {
-  OK = 0, BAD_ARGUMENT = 1, BAD_SHAPE = 2, MISSING_KEY = 3, SHAPE_MISMATCH = 4,
-  HIP_ERROR = 5, NONFINITE = 6, IO_ERROR = 7, NOT_LOADED = 8
-};
-
-struct Error : std::runtime_error {
-  int code;
-  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
-};
+// --- errors (errors.h: Status, Error, SPLAT_CHECK) ------------------------------------------
 
 #define SPLAT_HIP(expr)                                                                   \
   do {                                                                                     \
     hipError_t e_ = (expr);                                                                \
     if (e_ != hipSuccess)                                                                  \
       throw ::splat::Error(::splat::HIP_ERROR, std::string(#expr) + ": " + hipGetErrorString(e_)); \
-  } while (0)
-
-#define SPLAT_CHECK(cond, code, msg)                                                      \
-  do {                                                                                     \
-    if (!(cond)) throw ::splat::Error((code), (msg));                                     \
   } while (0)
 
 // --- bf16 conversion ----------------------------------------------------------------------

@@ -3,6 +3,7 @@
 // [views, rows, cols, channels] (a token matrix of a patch grid IS its NHWC map).
 #pragma once
 
+#include <functional>
 #include "common.h"
 
 namespace splat {
@@ -127,6 +128,11 @@ void attention(const Exec& ex, const AttnArgs& a);
 constexpr size_t ATTN_SCRATCH_BYTES = size_t(64) << 20;
 constexpr int ATTN_SCRATCH_DEVICES = 64;
 void* attention_scratch(int device);
+// Runs `launch` (kernels on `stream` that use the device's scratch) after the previous eager
+// launch that used it, on whatever stream or context that ran, and leaves an event behind for the
+// next: calls from several contexts on one GPU are ordered by their host order. A launch under
+// stream capture is left to the caller's graph to order. Allocates nothing.
+void attention_scratch_ordered(int device, hipStream_t stream, const std::function<void()>& launch);
 
 // LayerNorm over the last dim of rows: out[r] = LN(in[row_in(r)]) * w + b (w/b nullable);
 // row_in(r) = (r / rm_P) * rm_n + rm_off + r % rm_P when rm_P > 0, else r.
@@ -192,6 +198,8 @@ void reconstruct_geometry(const Exec& ex, int V, int H, int W, const float* dept
 
 // RGBA u8 [V,H,W,4] -> normalised images [V,3,H,W] f32 and foreground [V,H,W] (NULL: skipped).
 void to_model_input(const Exec& ex, const uint8_t* rgba, int V, int H, int W, float* img, uint8_t* fg);
+// flags[v] = 1 if view v of the RGBA8 batch has a pixel with alpha >= 128, else 0.
+void foreground_any(const Exec& ex, const uint8_t* rgba, int V, int H, int W, int* flags);
 
 // The taps of one resize axis on the device: output coordinate o reads count[o] inputs from
 // first[o], weights w[offset[o] .. offset[o] + count[o]) (normalised, f32).

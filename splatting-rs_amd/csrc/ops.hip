@@ -1302,6 +1302,23 @@ void to_model_input(const Exec& ex, const uint8_t* rgba, int V, int H, int W, fl
   SPLAT_HIP(hipGetLastError());
 }
 
+// image_input.rs:196-197: whether view v keeps a foreground pixel (alpha >= 128) after cropping.
+// One block per view; every thread stops at its first foreground pixel, the block ORs them and
+// thread 0 writes flags[v] (0 or 1), so the flags need no clearing beforehand.
+__global__ void __launch_bounds__(256) foreground_any_kernel(const uint8_t* rgba, long hw, int* flags) {
+  const uchar4* px = reinterpret_cast<const uchar4*>(rgba) + long(blockIdx.x) * hw;
+  int any = 0;
+  for (long p = threadIdx.x; p < hw && !any; p += blockDim.x) any = px[p].w >= 128;
+  any = __syncthreads_or(any);
+  if (threadIdx.x == 0) flags[blockIdx.x] = any ? 1 : 0;
+}
+
+void foreground_any(const Exec& ex, const uint8_t* rgba, int V, int H, int W, int* flags) {
+  if (ex.dry || V == 0) return;
+  hipLaunchKernelGGL(foreground_any_kernel, dim3(V), dim3(256), 0, ex.stream, rgba, long(H) * W, flags);
+  SPLAT_HIP(hipGetLastError());
+}
+
 // ---------------------------------------------------------------------------------------
 // image 0.25.10 imageops::resize on RGBA8 (sample.rs: vertical_sample, then horizontal_sample):
 // pass 1 tmp[y, x] = sum_i w_y[i] * src[first_y + i, x] in f32, taps in order from 0; pass 2

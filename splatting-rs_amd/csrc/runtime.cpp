@@ -505,111 +505,6 @@ FusionW load_fusion(Loader& L, const std::string& p, int F, bool skip) {
   return f;
 }
 
-// --- host tables ---------------------------------------------------------------------------
-
-namespace {
-
-constexpr int TRAINED_GRID = 37;
-
-std::array<double, 4> bicubic_weights(double t) {
-  const double a = -0.75;
-  auto near = [a](double x) { return ((a + 2.0) * x - (a + 3.0)) * x * x + 1.0; };
-  auto far = [a](double x) { return ((a * x - 5.0 * a) * x + 8.0 * a) * x - 4.0 * a; };
-  return {far(t + 1.0), near(t), near(1.0 - t), far(2.0 - t)};
-}
-
-struct Taps {
-  int idx[4];
-  double w[4];
-};
-
-std::vector<Taps> bicubic_taps(int in, int out, double scale) {
-  std::vector<Taps> taps(out);
-  for (int o = 0; o < out; ++o) {
-    const double src = (o + 0.5) / scale - 0.5;
-    const double fl = std::floor(src);
-    auto w = bicubic_weights(src - fl);
-    for (int i = 0; i < 4; ++i) {
-      long v = long(fl) + i - 1;
-      taps[o].idx[i] = int(std::min<long>(std::max<long>(v, 0), in - 1));
-      taps[o].w[i] = w[i];
-    }
-  }
-  return taps;
-}
-
-}  // namespace
-
-// mapanything-rs/src/dinov2.rs:42-76 (separable bicubic, f64, columns then rows) applied as
-// depthanything3-rs/src/backbone.rs:94-112: class slot kept, scale (out + 0.1) / 37.
-std::vector<float> resize_pos_embed(const std::vector<float>& pos, int dim, int rows, int cols) {
-  const int G = TRAINED_GRID;
-  std::vector<float> out(size_t(1 + rows * cols) * dim);
-  std::memcpy(out.data(), pos.data(), sizeof(float) * dim);
-  if (rows == G && cols == G) {
-    std::memcpy(out.data(), pos.data(), sizeof(float) * out.size());
-    return out;
-  }
-  const float* grid = pos.data() + dim;
-  auto ct = bicubic_taps(G, cols, (cols + 0.1) / G);
-  std::vector<double> horiz(size_t(G) * cols * dim, 0.0);
-  for (int r = 0; r < G; ++r)
-    for (int oc = 0; oc < cols; ++oc) {
-      double* dst = &horiz[(size_t(r) * cols + oc) * dim];
-      for (int t = 0; t < 4; ++t) {
-        const float* src = grid + (size_t(r) * G + ct[oc].idx[t]) * dim;
-        for (int c = 0; c < dim; ++c) dst[c] += ct[oc].w[t] * double(src[c]);
-      }
-    }
-  auto rt = bicubic_taps(G, rows, (rows + 0.1) / G);
-  for (int orow = 0; orow < rows; ++orow)
-    for (int oc = 0; oc < cols; ++oc) {
-      float* dst = &out[(1 + size_t(orow) * cols + oc) * dim];
-      for (int c = 0; c < dim; ++c) {
-        double s = 0.0;
-        for (int t = 0; t < 4; ++t) s += rt[orow].w[t] * horiz[(size_t(rt[orow].idx[t]) * cols + oc) * dim + c];
-        dst[c] = float(s);
-      }
-    }
-  return out;
-}
-
-// depthanything3-rs/src/rope.rs:26-54: angle = pos * 100^(-p/16) in f64, stored f32.
-std::vector<float> rope_table(int npos) {
-  std::vector<float> t(size_t(2) * npos * 16);
-  for (int pos = 0; pos < npos; ++pos)
-    for (int p = 0; p < 16; ++p) {
-      const double ang = double(pos) * (1.0 / std::pow(100.0, double(p) / 16.0));
-      t[size_t(pos) * 16 + p] = float(std::cos(ang));
-      t[size_t(npos) * 16 + size_t(pos) * 16 + p] = float(std::sin(ang));
-    }
-  return t;
-}
-
-// depthanything3-rs/src/uv_embed.rs:14-53, laid out [pixel][channel].
-std::vector<float> uv_table(int channels, int rows, int cols, double aspect) {
-  const double diag = std::sqrt(aspect * aspect + 1.0);
-  const double span[2] = {aspect / diag, 1.0 / diag};
-  auto coord = [&](int i, int count, int axis) {
-    const double edge = span[axis] * (count - 1.0) / count;
-    return count == 1 ? -edge : -edge + 2.0 * edge * i / (count - 1.0);
-  };
-  const int half = channels / 2, q = half / 2;
-  std::vector<float> t(size_t(rows) * cols * channels);
-  for (int r = 0; r < rows; ++r)
-    for (int c = 0; c < cols; ++c) {
-      float* dst = &t[(size_t(r) * cols + c) * channels];
-      const double pos[2] = {coord(c, cols, 0), coord(r, rows, 1)};
-      for (int axis = 0; axis < 2; ++axis)
-        for (int k = 0; k < q; ++k) {
-          const double ang = pos[axis] / std::pow(100.0, double(k) / q);
-          dst[axis * half + k] = float(std::sin(ang)) * 0.1f;
-          dst[axis * half + q + k] = float(std::cos(ang)) * 0.1f;
-        }
-    }
-  return t;
-}
-
 // --- context ---------------------------------------------------------------------------------
 
 Context::Context(int dev) : device(dev) {

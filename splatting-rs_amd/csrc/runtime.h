@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "../../include/splathip.h"
+#include "host_tables.h"
 #include "kernels.h"
 #include "safetensors.h"
 
@@ -154,19 +155,13 @@ void block_ln_refresh(Context& ctx, int dt, const float* x, int rows, int dim, B
 
 // --- image preprocessing (preprocess.cpp) -----------------------------------------------------
 
-// Host taps of one resize axis (image 0.25.10 sample.rs): output o reads count[o] inputs from
-// first[o] with the normalised weights w[offset[o] ..].
-struct ResizeTapsHost {
-  std::vector<int> first, count, offset;
-  std::vector<float> w;
-};
-ResizeTapsHost resize_taps(int in, int out, int filter);
-void da3_model_input_size(int width, int height, int& bw, int& bh, int& dw, int& dh);
-int da3_resize_filter(int w, int h, int nw, int nh);
-void ma_input_size(int n, const int* widths, const int* heights, int& width, int& height);
-void ma_cover(int w, int h, int width, int height, int& rw, int& rh, int& left, int& top, int& filter);
+// (resize_taps and the size rules: host_tables.h)
 // Device RGBA8 [h, w, 4] -> device RGBA8 [nh, nw, 4] (synchronises the context's stream).
 void resize_device(Context& c, const uint8_t* src, int w, int h, uint8_t* dst, int nw, int nh, int filter);
+// mapanything-rs/src/image_input.rs:195-216 on a device RGBA8 batch [V, H, W, 4]: the normalised
+// images and foreground, and the reference's error when a view has no foreground pixel
+// (synchronises the context's stream).
+void model_input(Context& c, const uint8_t* rgba, int V, int H, int W, float* images, uint8_t* foreground);
 // The crates' preprocessing of decoded host RGBA8 images into the device model input.
 void da3_model_inputs(Context& c, int n, const uint8_t* const* rgba, const int* widths, const int* heights, float* images,
                       uint8_t* foreground, int& H, int& W);
@@ -391,10 +386,5 @@ void Context::run(const GraphKey& key, bool use_graph, F&& body) {
   graph_cache[key] = exec;
   SPLAT_HIP(hipGraphLaunch(exec, stream));
 }
-
-// Host tables shared by the models.
-std::vector<float> resize_pos_embed(const std::vector<float>& pos, int dim, int rows, int cols);  // [1+P, d]
-std::vector<float> rope_table(int npos);                                                        // [2][npos][16]
-std::vector<float> uv_table(int channels, int rows, int cols, double aspect);                   // [rows*cols, C]
 
 }  // namespace splat

@@ -5,9 +5,10 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cstdint>
 #include <cstring>
 
-#include "common.h"
+#include "errors.h"
 
 namespace splat {
 
@@ -18,6 +19,7 @@ namespace {
 struct Json {
   const char* p;
   const char* end;
+  int depth = 0;  // nesting of the value being skipped (a crafted header must not exhaust the stack)
 
   [[noreturn]] void fail(const char* what) { throw Error(IO_ERROR, std::string("safetensors header: ") + what); }
   void ws() {
@@ -44,8 +46,10 @@ struct Json {
           if (end - p < 5) fail("bad \\u escape");
           unsigned v = 0;
           for (int i = 1; i <= 4; ++i) {
-            char h = p[i];
-            v = v * 16 + (h >= '0' && h <= '9' ? h - '0' : (h | 32) - 'a' + 10);
+            const char h = p[i], l = char(h | 32);
+            if (h >= '0' && h <= '9') v = v * 16 + unsigned(h - '0');
+            else if (l >= 'a' && l <= 'f') v = v * 16 + unsigned(l - 'a' + 10);
+            else fail("bad \\u escape");
           }
           p += 4;
           if (v < 0x80) s += char(v);
@@ -68,13 +72,26 @@ struct Json {
     if (p < end && *p == '-') { neg = true; ++p; }
     if (p >= end || *p < '0' || *p > '9') fail("expected an integer");
     int64_t v = 0;
-    while (p < end && *p >= '0' && *p <= '9') v = v * 10 + (*p++ - '0');
+    while (p < end && *p >= '0' && *p <= '9') {
+      const int digit = *p++ - '0';
+      if (v > (INT64_MAX - digit) / 10) fail("integer out of range");
+      v = v * 10 + digit;
+    }
     return neg ? -v : v;
   }
   void skip_value() {
     ws();
     if (p >= end) fail("truncated");
+    if (*p == '{' || *p == '[') {
+      if (++depth > 64) fail("nested too deeply");
+      skip_container();
+      --depth;
+      return;
+    }
     if (*p == '"') { str(); return; }
+    while (p < end && *p != ',' && *p != '}' && *p != ']') ++p;
+  }
+  void skip_container() {
     if (*p == '{') {
       ++p;
       if (peek('}')) { ++p; return; }
@@ -87,9 +104,7 @@ struct Json {
       if (peek(']')) { ++p; return; }
       do { skip_value(); } while (peek(',') && ++p);
       expect(']');
-      return;
     }
-    while (p < end && *p != ',' && *p != '}' && *p != ']') ++p;
   }
   std::vector<int64_t> int_array() {
     std::vector<int64_t> v;
@@ -107,6 +122,24 @@ size_t dtype_bytes(const std::string& dt) {
   if (dt == "F64" || dt == "I64" || dt == "U64") return 8;
   if (dt == "U8" || dt == "I8" || dt == "BOOL") return 1;
   return 0;
+}
+
+float bf16_to_f32(uint16_t h) {
+  const uint32_t u = uint32_t(h) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// The element count of a header shape, or -1 if a dimension is negative or the byte size of the
+// tensor (count times `elem` bytes) does not fit in int64_t.
+int64_t checked_numel(const std::vector<int64_t>& shape, size_t elem) {
+  int64_t n = 1;
+  for (int64_t s : shape)
+    if (s < 0 || __builtin_mul_overflow(n, s, &n)) return -1;
+  int64_t bytes;
+  if (__builtin_mul_overflow(n, int64_t(elem), &bytes)) return -1;
+  return n;
 }
 
 float half_to_f32(uint16_t h) {
@@ -197,7 +230,9 @@ void SafeTensors::parse(const uint8_t* base, size_t len) {
                 "safetensors: bad data_offsets for " + name);
     const size_t eb = dtype_bytes(t.dtype);
     SPLAT_CHECK(eb != 0, IO_ERROR, "safetensors: unsupported dtype " + t.dtype + " for " + name);
-    SPLAT_CHECK(size_t(offs[1] - offs[0]) == size_t(t.numel()) * eb, IO_ERROR, "safetensors: size mismatch for " + name);
+    const int64_t n = checked_numel(t.shape, eb);
+    SPLAT_CHECK(n >= 0, IO_ERROR, "safetensors: bad shape " + shape_str(t.shape) + " for " + name);
+    SPLAT_CHECK(uint64_t(offs[1] - offs[0]) == uint64_t(n) * eb, IO_ERROR, "safetensors: size mismatch for " + name);
     t.data = data + offs[0];
     t.nbytes = size_t(offs[1] - offs[0]);
     tensors_[name] = std::move(t);
@@ -223,7 +258,7 @@ std::vector<float> SafeTensors::f32(const std::string& name, const std::vector<i
     for (size_t i = 0; i < n; ++i) {
       uint16_t v;
       std::memcpy(&v, t.data + 2 * i, 2);
-      out[i] = bf2f(v);
+      out[i] = bf16_to_f32(v);
     }
   } else if (t.dtype == "F16") {
     for (size_t i = 0; i < n; ++i) {

@@ -16,6 +16,8 @@ struct StTensor {
   std::vector<int64_t> shape;
   const uint8_t* data = nullptr;
   size_t nbytes = 0;
+  // Parsed shapes are checked (no negative dimension, byte size within int64_t), so this
+  // product does not overflow.
   int64_t numel() const {
     int64_t n = 1;
     for (auto s : shape) n *= s;
@@ -34,6 +36,11 @@ class SafeTensors {
   void open_bytes(const uint8_t* bytes, size_t len);   // copies the bytes
 
   bool has(const std::string& name) const { return tensors_.count(name) != 0; }
+  std::vector<std::string> names() const {
+    std::vector<std::string> r;
+    for (const auto& kv : tensors_) r.push_back(kv.first);
+    return r;
+  }
   const StTensor& get(const std::string& name) const;  // throws MISSING_KEY
   // The tensor converted to f32, after checking its shape (throws SHAPE_MISMATCH).
   std::vector<float> f32(const std::string& name, const std::vector<int64_t>& shape) const;
