@@ -20,9 +20,14 @@ Pinned (tests/test_oracle_preprocess.py) by the reference's own unit tests of th
 at the same size, constant images stay constant, a Triangle halving averages with weights
 (1, 3, 3, 1) / 8, Triangle enlarging interpolates linearly, CatmullRom reproduces linear ramps,
 every filter's weights sum to one and are symmetric, the separable passes equal the 2-D
-weighted sum. What only the crate itself could pin (its exact f32 rounding sequence, the sin
-of Lanczos3) is "parity unpinned"; the restatement follows the published source's order.
+weighted sum. What only the crate itself could pin (its exact f32 rounding sequence) is
+"parity unpinned"; the restatement follows the published source's order. The Lanczos3 sinc takes
+its sine from the C library's `sinf`, which is what Rust's `f32::sin` calls on Linux (and what the
+library's host code calls), not numpy's float32 `np.sin`, whose vectorised routine differs from it
+in the last bit for some arguments.
 """
+import ctypes
+import ctypes.util
 import math
 
 import numpy as np
@@ -30,6 +35,10 @@ import numpy as np
 from .common import to_model_input
 
 TRIANGLE, CATMULLROM, LANCZOS3 = 1, 2, 3
+_LIBM = ctypes.CDLL(ctypes.util.find_library("m") or "libm.so.6")
+_sinf = _LIBM.sinf
+_sinf.restype = ctypes.c_float
+_sinf.argtypes = [ctypes.c_float]
 _SUPPORT = {TRIANGLE: 1.0, CATMULLROM: 2.0, LANCZOS3: 3.0}
 F = np.float32
 
@@ -55,7 +64,7 @@ def _kernel(filter_type, x):
     def sinc(t):
         t = F(t)
         s = F(t * F(math.pi))
-        return F(1.0) if t == F(0.0) else F(F(np.sin(s)) / s)
+        return F(1.0) if t == F(0.0) else F(F(_sinf(s)) / s)
 
     return F(sinc(x) * sinc(F(x / F(3.0)))) if a < F(3.0) else F(0.0)
 
