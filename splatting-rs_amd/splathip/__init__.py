@@ -260,6 +260,14 @@ class Context:
                                                     DTYPES[dtype]))
         self.ma_spec = spec or specs.MA_SPECS["reference"]
 
+    def load_mapanything_bytes(self, data: bytes, spec: Optional[specs.MaSpec] = None, dtype: str = "bf16"):
+        """A safetensors checkpoint held in memory (the wasm worker's fetched bytes)."""
+        buf = np.frombuffer(data, np.uint8)
+        cs = MaSpecC.from_spec(spec) if spec is not None else None
+        self.check(self._lib.splat_load_mapanything_bytes(self.handle, _ptr(buf), buf.size,
+                                                          C.byref(cs) if cs else None, DTYPES[dtype]))
+        self.ma_spec = spec or specs.MA_SPECS["reference"]
+
     @staticmethod
     def _cameras(intrinsics, V: int):
         """None, or one entry per view: None (unknown camera) or (fx, fy, cx, cy)."""
