@@ -239,6 +239,18 @@ template <int G> __device__ __forceinline__ float group_sum(float v) {
 
 constexpr int slab_ld(int tn) { return tn * 32 + 4; }  // +4 floats: conflict-free 16-byte row reads
 
+// A __shared__ float array of N elements, or none (nullptr) when N is 0: a kernel whose operand
+// ring fills the LDS declares nothing else.
+template <int N> struct LdsFloats {
+  __device__ static float* get() {
+    __shared__ __attribute__((aligned(16))) float a[N];
+    return a;
+  }
+};
+template <> struct LdsFloats<0> {
+  __device__ static float* get() { return nullptr; }
+};
+
 
 template <int TM, int TN, bool L16>
 __device__ __forceinline__ void stage_slab(const f32x16 (&acc)[TM][TN], int i, float* slab, int lane) {
@@ -846,7 +858,11 @@ constexpr int A_CONV_TAP = 2;
 // byte for byte; BK counts elements (128-byte rows: 64 bf16 or 32 fp32).
 // MINB: blocks per CU the register allocation must allow (2 for a tile whose LDS ring lets two
 // blocks share a CU).
-template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int AMODE, bool RELU, int EPI, int MINB>
+// AR: ring stages of the A tiles (STAGES those of W). AR = 3 with two W stages (the 256x256 tile,
+// exactly the 160 KB of LDS): the loads of A tile kt+2 stream during tile kt, so the load path
+// does not drain at every barrier; only the W half is issued after it.
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int AMODE, bool RELU, int EPI, int MINB,
+          int AR = STAGES>
 __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const GemmArgs p, int tiles_m, int tiles_n) {
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32, NW = WM * WN;
   constexpr int ES = sizeof(T), KE = 16 / ES;  // bytes per element, elements per 16-byte chunk
@@ -866,15 +882,23 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   static_assert(AL * NW * RPI == BM && BL * NW * RPI == BN, "tile rows split evenly over the waves' loads");
   static_assert(((NW * RPI) >> SH) % CPR == 0, "a load's swizzle slot is the same for every instruction");
   constexpr int STAGE = (BM + BN) * RB;
+  constexpr bool SPLITR = AR != STAGES;
+  static_assert(!SPLITR || (STAGES == 2 && AR == 3), "split ring: three A stages, two W stages");
+  constexpr int RING = SPLITR ? AR * BM * RB + STAGES * BN * RB : STAGES * STAGE;
   static_assert((STAGES - 1) * LPT <= 63, "vmcnt range");
-  static_assert(STAGES * STAGE >= NW * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the ring");
+  static_assert(RING >= NW * 32 * slab_ld(TN) * 4, "epilogue slabs reuse the ring");
   static_assert(EPI != EPI_LN || NW * 64 >= BM, "folded LayerNorm: a thread per tile row");
-  static_assert(EPI != EPI_LN || STAGES * STAGE >= (NW * 32 * slab_ld(TN) + (WN + 1) / 2 * BM * 4) * 4,
+  // EPI_LN past the slabs: the qk-norm exchange, then (split ring) the rows' (rstd, -rstd * mean)
+  constexpr int XCH = (WN + 1) / 2 * BM * 4;
+  static_assert(EPI != EPI_LN || RING >= (NW * 32 * slab_ld(TN) + XCH + (SPLITR ? 2 * BM : 0)) * 4,
                 "qk-norm exchange past the epilogue slabs");
-  static_assert(EPI != EPI_RESLN || STAGES * STAGE >= (NW * 32 * slab_ld(TN) + BM * (BN / 32) * 2) * 4,
+  static_assert(EPI != EPI_RESLN || RING >= (NW * 32 * slab_ld(TN) + BM * (BN / 32) * 2) * 4,
                 "row statistics: the 32-column sums past the epilogue slabs");
-  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
-  __shared__ __attribute__((aligned(16))) float lnab[EPI == EPI_LN ? 2 * BM : 2];  // (rstd, -rstd * mean) a row
+  __shared__ __attribute__((aligned(1024))) char smem[RING];
+  // (rstd, -rstd * mean) a row (EPI_LN): its own array, or with the split ring in the ring past the
+  // slabs and the exchange, written after the main loop
+  float* lnab = SPLITR ? reinterpret_cast<float*>(smem) + NW * 32 * slab_ld(TN) + XCH
+                       : LdsFloats<EPI == EPI_LN ? 2 * BM : 0>::get();
 
   // the wave index is uniform: every LDS destination of the DMA loads is scalar arithmetic
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -965,7 +989,9 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   // have voffset OOB.
   auto issue_one = [&](int kr, int stage, int l, auto full) {
     constexpr bool FULL = decltype(full)::value;
-    const uint32_t sb = lds_addr(smem + stage * STAGE);
+    // A rows at sb + ..., W rows at sb + BM * RB + ... (split ring: A slot kr % AR, W slot `stage`)
+    const uint32_t sb = SPLITR ? lds_addr(smem + (l < AL ? (kr % AR) * BM * RB : AR * BM * RB + stage * BN * RB - BM * RB))
+                               : lds_addr(smem + stage * STAGE);
     const int kt = kt0 + kr;
     const int k = kt * BK + c * KE;
     const bool kin = FULL || k < kend;
@@ -1038,6 +1064,7 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
 #pragma unroll
     for (int l = 0; l < LPT; ++l) issue_one(s, s, l, std::false_type{});
   wait_vmcnt<(AHEAD - 1) * LPT>();
+  float ln_rstd = 0.f, ln_shift = 0.f;
   if constexpr (EPI == EPI_LN) {
     if (tid < BM) {
       float s = 0.f, q = 0.f;
@@ -1047,9 +1074,12 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
         q += lnv[j].y;
       }
       const float inv = 1.f / float(p.K), mean = s * inv;
-      const float rstd = rsqrtf(fmaxf(q * inv - mean * mean, 0.f) + p.ln_eps);
-      lnab[2 * tid] = rstd;
-      lnab[2 * tid + 1] = -rstd * mean;
+      ln_rstd = rsqrtf(fmaxf(q * inv - mean * mean, 0.f) + p.ln_eps);
+      ln_shift = -ln_rstd * mean;
+      if constexpr (!SPLITR) {
+        lnab[2 * tid] = ln_rstd;
+        lnab[2 * tid + 1] = ln_shift;
+      }
     }
   }
   __syncthreads();
@@ -1063,16 +1093,24 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   // Fragment f of a k-step in the order the MFMAs (i outer, j inner) first use them: the A
   // fragments of tile row 0, then every W fragment, then the other A ones, so that the first
   // MFMAs of a step wait for few reads. Fragment rows are 32 / FH apart.
-  auto read_frag = [&](const char* sb, int off, int slot, int f) {
-    constexpr int RS = 32 / FH * RB;
-    if (f < FH) fa[slot][f] = *reinterpret_cast<const uint4*>(sb + arow0 + f * RS + off);
-    else if (f < FH + TN * FH) fb[slot][f - FH] = *reinterpret_cast<const uint4*>(sb + brow0 + (f - FH) * RS + off);
-    else fa[slot][f - TN * FH] = *reinterpret_cast<const uint4*>(sb + arow0 + (f - TN * FH) * RS + off);
+  // k-tile kt's A rows at abase(kt) + arow0.., its W rows at wbase(kt) + brow0.. (brow0 counts
+  // the BM A rows of a whole stage)
+  auto abase = [&](int kt) -> const char* { return smem + (SPLITR ? (kt % AR) * BM * RB : (kt % STAGES) * STAGE); };
+  auto wbase = [&](int kt) -> const char* {
+    return SPLITR ? smem + AR * BM * RB + (kt % STAGES) * BN * RB - BM * RB : smem + (kt % STAGES) * STAGE;
   };
-  auto read_frags = [&](const char* sb, int s, int slot) {
+  auto read_frag = [&](int kt, int off, int slot, int f) {
+    constexpr int RS = 32 / FH * RB;
+    const char* sa = abase(kt);
+    const char* sw_ = wbase(kt);
+    if (f < FH) fa[slot][f] = *reinterpret_cast<const uint4*>(sa + arow0 + f * RS + off);
+    else if (f < FH + TN * FH) fb[slot][f - FH] = *reinterpret_cast<const uint4*>(sw_ + brow0 + (f - FH) * RS + off);
+    else fa[slot][f - TN * FH] = *reinterpret_cast<const uint4*>(sa + arow0 + (f - TN * FH) * RS + off);
+  };
+  auto read_frags = [&](int kt, int s, int slot) {
     const int off = step_off(s);
 #pragma unroll
-    for (int f = 0; f < (TM + TN) * FH; ++f) read_frag(sb, off, slot, f);
+    for (int f = 0; f < (TM + TN) * FH; ++f) read_frag(kt, off, slot, f);
   };
   // the products of tile pair (i, j) for the k-step whose fragments sit in `slot`
   auto mma = [&](int i, int j, int slot) {
@@ -1081,13 +1119,12 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
     else
       Mfma<T>::mma(acc[i][j], fa[slot][i], fb[slot][j]);
   };
-  read_frags(smem, 0, 0);
+  read_frags(0, 0, 0);
   // One k-tile; the last one is peeled (HAS_NEXT false) so that each step's reads and MFMAs
   // share a basic block and the LDS waits stay exact.
   constexpr int MM = TM * TN, NF = (TM + TN) * FH, CUR = (KS - 1) & 1;
   auto tile = [&](int kt, auto has_next, auto full) {
     constexpr bool HAS_NEXT = decltype(has_next)::value;
-    const char* sb = smem + (kt % STAGES) * STAGE;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       // hard fence: the reads below belong to this step's region and nothing moves across
@@ -1096,10 +1133,11 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
 #pragma unroll
         for (int i = 0; i < TM * FH; ++i) fa[s & 1][i] = Mfma<T>::relu(fa[s & 1][i]);
       }
-      if (SPREAD && s + 1 < KS) {
-        // this step's share of the loads of tile kt + AHEAD and the reads of the next step's
-        // fragments, spread between the MFMAs
-        const int L0 = s * LPT / (KS - 1), L1 = (s + 1) * LPT / (KS - 1);
+      if ((SPREAD || (SPLITR && HAS_NEXT)) && s + 1 < KS) {
+        // this step's share of the loads of tile kt + AHEAD (split ring: of the A rows of tile
+        // kt + 2 only) and the reads of the next step's fragments, spread between the MFMAs
+        constexpr int LS = SPLITR ? AL : LPT;
+        const int L0 = s * LS / (KS - 1), L1 = (s + 1) * LS / (KS - 1);
         const int off = step_off(s + 1);
 #pragma unroll
         for (int q = 0; q < MM; ++q) {
@@ -1108,11 +1146,11 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
           for (int l = L0 + q * (L1 - L0) / MM; l < L0 + (q + 1) * (L1 - L0) / MM; ++l)
             issue_one(kt + AHEAD, (kt + AHEAD) % STAGES, l, full);
 #pragma unroll
-          for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) read_frag(sb, off, (s + 1) & 1, r);
+          for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) read_frag(kt, off, (s + 1) & 1, r);
           __builtin_amdgcn_sched_barrier(0);
         }
       } else if (s + 1 < KS || !HAS_NEXT) {
-        if (s + 1 < KS) read_frags(sb, s + 1, (s + 1) & 1);
+        if (s + 1 < KS) read_frags(kt, s + 1, (s + 1) & 1);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -1131,19 +1169,21 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
         // resident (tiles kt+2 .. kt+STAGES-1 may still be in flight). With two stages the
         // loads of tile kt+2 and the reads of the next tile's first fragments are spread
         // between this step's MFMAs, in a fixed order; with more, only the reads.
-        wait_vmcnt<(STAGES - 2) * LPT>();
+        // Split ring: tile kt+1 is resident once at most the AL loads of A tile kt+2 are in
+        // flight; then the W loads of tile kt+2 go out.
+        wait_vmcnt<SPLITR ? AL : (STAGES - 2) * LPT>();
         __syncthreads();
-        const char* nb = smem + ((kt + 1) % STAGES) * STAGE;
         const int off0 = step_off(0);
+        constexpr int LB = SPLITR ? AL : 0, LN_ = LPT - LB;
 #pragma unroll
         for (int q = 0; q < MM; ++q) {
           mma(q / TN, q % TN, CUR);
           if constexpr (!SPREAD) {
 #pragma unroll
-            for (int l = q * LPT / MM; l < (q + 1) * LPT / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l, full);
+            for (int l = LB + q * LN_ / MM; l < LB + (q + 1) * LN_ / MM; ++l) issue_one(kt + STAGES, kt % STAGES, l, full);
           }
 #pragma unroll
-          for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) read_frag(nb, off0, 0, r);
+          for (int r = q * NF / MM; r < (q + 1) * NF / MM; ++r) read_frag(kt + 1, off0, 0, r);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -1157,16 +1197,24 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   tile(nk - 1, std::false_type{}, std::false_type{});
   wait_vmcnt<0>();  // the zero-fill loads past the last tile must land before the ring is reused
   __syncthreads();  // every wave is past its last read of the ring before slabs reuse it
+  if constexpr (SPLITR && EPI == EPI_LN) {
+    if (tid < BM) {
+      lnab[2 * tid] = ln_rstd;
+      lnab[2 * tid + 1] = ln_shift;
+    }
+    __syncthreads();
+  }
   if constexpr (sizeof(T) == 4) __builtin_amdgcn_s_setprio(0);
   if constexpr (EPI == EPI_HEAD) {
-    static_assert(NW * 32 * slab_ld(TN) * 4 + BM * WN * 6 * 4 <= STAGES * STAGE, "head epilogue LDS");
+    static_assert(NW * 32 * slab_ld(TN) * 4 + BM * WN * 6 * 4 <= RING, "head epilogue LDS");
     head_epilogue<T, BM, BN, WM, WN, TM, TN, L16>(p, acc, m0, wm, wn, reinterpret_cast<float*>(smem), wave, lane, tid);
   } else {
     float* slab = reinterpret_cast<float*>(smem) + wave * 32 * slab_ld(TN);
     constexpr int LNLD = BN / 32;  // 32-column sums per tile row (EPI_RESLN)
     float* lnp = reinterpret_cast<float*>(smem) + NW * 32 * slab_ld(TN);
     epilogue<T, TM, TN, EPI, L16>(p, acc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), slab, lane, p.epi_vec,
-                             EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr, lnab + wm * (BM / WM) * 2,
+                             EPI == EPI_PART ? p.part + long(split) * p.M * p.ldp : nullptr,
+                             EPI == EPI_LN ? lnab + wm * (BM / WM) * 2 : nullptr,
                              lnp + (wm * (BM / WM) * LNLD + wn * (BN / WN) / 32) * 2, LNLD,
                              lnp + (wn / 2) * BM * 4, wm * (BM / WM));
     if constexpr (EPI == EPI_RESLN) {
@@ -1287,7 +1335,7 @@ static void xcd_tile_map(GemmArgs& b, int tm, int tn, int bm, int bn) {
 // maps whose Cin is a multiple of 32 but not of 64).
 // Returns whether the launch wrote the row statistics (and copy) a producer (ln_out) asks for.
 template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 128 / sizeof(T), int MINB = 1,
-          bool TAP_ONLY = false>
+          bool TAP_ONLY = false, int AR = STAGES>
 static bool launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   static_assert(MINB == 1 || MINB * STAGES * (BM + BN) * BK * sizeof(T) <= 160 * 1024, "LDS of MINB blocks per CU");
   const int tm = cdiv(a.M, BM), tn = cdiv(a.N, BN);
@@ -1306,7 +1354,7 @@ static bool launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
   }
   dim3 grid(tm * tn * S);
 #define SPLAT_GO(AM, RL, EP) \
-  hipLaunchKernelGGL((gemm_mfma_kernel<T, BM, BN, WM, WN, STAGES, BK, AM, RL, EP, MINB>), grid, dim3(WM * WN * 64), 0, ex.stream, \
+  hipLaunchKernelGGL((gemm_mfma_kernel<T, BM, BN, WM, WN, STAGES, BK, AM, RL, EP, MINB, AR>), grid, dim3(WM * WN * 64), 0, ex.stream, \
                      b, tm, tn)
   // Convolutions take the per-tap path (A_CONV_TAP) when Cin is a multiple of the k-tile, else
   // the per-lane im2col arithmetic (A_CONV, without ReLU-on-load: no such caller).
@@ -1490,7 +1538,9 @@ static bool launch_h16_auto(const Exec& ex, const GemmArgs& a) {
   switch (c) {
     case CFG_128x32: return launch_mfma<H, 128, 32, 4, 1, 2>(ex, a, S);
     case CFG_128x64: return launch_mfma<H, 128, 64, 2, 2, 2>(ex, a, S);
-    case CFG_256x256: return launch_mfma<H, 256, 256, 2, 4, 2>(ex, a, S);
+    // three A stages, two W stages (the whole 160 KB): 8192^3 990 -> 950 us, 8192x8192x2048 233 ->
+    // 225 us; the C4 layer shapes (12-16 k-tiles a tile) unchanged
+    case CFG_256x256: return launch_mfma<H, 256, 256, 2, 4, 2, 64, 1, false, 3>(ex, a, S);
     case CFG_256x128: return launch_mfma<H, 256, 128, 4, 2, 3>(ex, a, S);
     case CFG_320x256: return launch_mfma<H, 320, 256, 2, 4, 2>(ex, a, S);
     case CFG_320x128: return launch_mfma<H, 320, 128, 2, 4, 2>(ex, a, S);
