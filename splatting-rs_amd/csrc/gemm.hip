@@ -1345,7 +1345,10 @@ static bool launch_mfma(const Exec& ex, const GemmArgs& a, int S) {
               "gemm: a folded LayerNorm needs plain rows, a vectorisable epilogue and no split-K");
   GemmArgs b = a;
   b.tgroup = 8;
-  b.tcontig = (tm * tn) % 8 == 0;
+  // Convolutions: each XCD takes a contiguous run of tiles, i.e. a band of output rows, so the
+  // halo rows two neighbouring tiles share are fetched into one L2 (xcd_contiguous spreads a tile
+  // count that is not a multiple of 8 over the XCDs in runs that differ by at most one tile).
+  b.tcontig = a.amode != A_ROWS || (tm * tn) % 8 == 0;
   if (a.amode == A_ROWS && S == 1) xcd_tile_map(b, tm, tn, BM, BN);
   if (S > 1) {
     b.part = static_cast<float*>(ex.ws->ptr);
