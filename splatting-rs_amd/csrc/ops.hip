@@ -721,8 +721,18 @@ void small_linear(const Exec& ex, int wdt, const float* x, long ldx, int M, int 
 // ---------------------------------------------------------------------------------------
 // depthanything3-rs/src/reference_view.rs:38-80 on the device, in f64: Gram matrix and row
 // sums of the class tokens, then mean cosine similarity, norm and unbiased variance of the
-// unit token, each min-max scaled, balance = sum |x - 0.5|, first argmin.
+// unit token, each min-max scaled, balance = sum |x - 0.5|, first argmin. Up to REF_MAX_VIEWS
+// views one block holds the Gram matrix in shared memory; beyond that one block per view
+// computes its metrics (the same dot products, sums and order, so the same bits) into the
+// workspace and one more block scales them and takes the argmin.
 constexpr int REF_MAX_VIEWS = 64;
+
+// Sum over the lanes of a dot product of two dim-long rows (lane-strided, then the wave sum).
+__device__ inline double row_dot_d(const float* a, const float* b, int dim, int lane) {
+  double s = 0.0;
+  for (int c = lane; c < dim; c += 64) s += double(a[c]) * double(b[c]);
+  return wave_sum_d(s);
+}
 
 __global__ void __launch_bounds__(1024) ref_view_kernel(const float* xs, int V, int n, int dim, int strategy, int* ref) {
   __shared__ double gram[REF_MAX_VIEWS * REF_MAX_VIEWS];
@@ -796,10 +806,98 @@ __global__ void __launch_bounds__(1024) ref_view_kernel(const float* xs, int V, 
   }
 }
 
+// Block i: view i's mean cosine similarity, norm and variance into met[0 / V / 2V + i]. The
+// similarity terms of REF_CHUNK views at a time go through shared memory and thread 0 adds
+// them in view order, skipping i.
+constexpr int REF_CHUNK = 256;
+
+__global__ void __launch_bounds__(256) ref_view_metrics_kernel(const float* xs, int V, int n, int dim, double* met) {
+  __shared__ double term[REF_CHUNK];
+  __shared__ double own[2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int i = blockIdx.x;
+  const float* a = xs + (long)i * n * dim;
+  if (wave == 0) {
+    const double g = row_dot_d(a, a, dim, lane);
+    if (lane == 0) own[0] = g;
+  } else if (wave == 1) {
+    double r = 0.0;
+    for (int c = lane; c < dim; c += 64) r += double(a[c]);
+    r = wave_sum_d(r);
+    if (lane == 0) own[1] = r;
+  }
+  __syncthreads();
+  const double nrm = sqrt(own[0]);
+  double s = 0.0;
+  for (int j0 = 0; j0 < V; j0 += REF_CHUNK) {
+    const int cnt = min(REF_CHUNK, V - j0);
+    for (int t = wave; t < cnt; t += nw) {
+      const int j = j0 + t;
+      const float* b = xs + (long)j * n * dim;
+      const double gij = row_dot_d(a, b, dim, lane);
+      const double gjj = row_dot_d(b, b, dim, lane);
+      if (lane == 0) term[t] = gij / (nrm * sqrt(gjj));
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int t = 0; t < cnt; ++t)
+        if (j0 + t != i) s += term[t];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double mean = own[1] / nrm / dim;
+    const double sq = own[0] / (nrm * nrm);
+    met[i] = s / (V - 1);
+    met[V + i] = nrm;
+    met[2 * V + i] = (sq - dim * mean * mean) / (dim - 1);
+  }
+}
+
+// Min-max range of each metric (three threads), then the balance and its first argmin in
+// view order (thread 0).
+__global__ void __launch_bounds__(64) ref_view_pick_kernel(const double* met, int V, int* ref) {
+  __shared__ double lohi[3][2];
+  const int k = threadIdx.x;
+  if (k < 3) {
+    double lo = INFINITY, hi = -INFINITY;
+    for (int v = 0; v < V; ++v) { lo = fmin(lo, met[k * V + v]); hi = fmax(hi, met[k * V + v]); }
+    lohi[k][0] = lo;
+    lohi[k][1] = hi;
+  }
+  __syncthreads();
+  if (k == 0) {
+    int best = 0;
+    double best_b = 0.0;
+    for (int v = 0; v < V; ++v) {
+      double b = 0.0;
+      for (int m = 0; m < 3; ++m) b += fabs((met[m * V + v] - lohi[m][0]) / (lohi[m][1] - lohi[m][0] + 1e-8) - 0.5);
+      if (v == 0 || b < best_b) {
+        best = v;
+        best_b = b;
+      }
+    }
+    *ref = best;
+  }
+}
+
 void select_reference_view(const Exec& ex, const float* xs, int V, int n, int dim, int strategy, int* ref) {
-  SPLAT_CHECK(V <= REF_MAX_VIEWS, BAD_SHAPE, "reference-view selection supports at most 64 views");
-  if (ex.dry) return;
-  hipLaunchKernelGGL(ref_view_kernel, dim3(1), dim3(1024), 0, ex.stream, xs, V, n, dim, strategy, ref);
+  SPLAT_CHECK(V >= 1 && n >= 1 && dim >= 2, BAD_SHAPE, "reference-view selection: bad token shape");
+  const bool grid = V > REF_MAX_VIEWS && V >= 3 && strategy == 2;
+  const size_t bytes = size_t(3) * V * sizeof(double);
+  if (ex.dry) {
+    if (grid && ex.ws) ex.ws->need = std::max(ex.ws->need, bytes);
+    return;
+  }
+  if (!grid) {  // beyond REF_MAX_VIEWS only the fixed choices (first, middle) reach this kernel
+    hipLaunchKernelGGL(ref_view_kernel, dim3(1), dim3(1024), 0, ex.stream, xs, V, n, dim, strategy, ref);
+    SPLAT_HIP(hipGetLastError());
+    return;
+  }
+  SPLAT_CHECK(ex.ws && ex.ws->ptr && ex.ws->cap >= bytes, BAD_ARGUMENT,
+              "reference-view selection over more than 64 views needs the sized workspace");
+  double* met = static_cast<double*>(ex.ws->ptr);
+  hipLaunchKernelGGL(ref_view_metrics_kernel, dim3(V), dim3(256), 0, ex.stream, xs, V, n, dim, met);
+  hipLaunchKernelGGL(ref_view_pick_kernel, dim3(1), dim3(64), 0, ex.stream, met, V, ref);
   SPLAT_HIP(hipGetLastError());
 }
 

@@ -116,6 +116,22 @@ def test_da3_reference_view_strategies(ctx, da3_weights):
         _check_fp32(out, ref)
 
 
+@pytest.mark.parametrize("views", [64, 65, 300])
+def test_da3_reference_view_beyond_64_views(ctx, da3_weights, views):
+    """reference_view.rs:38-80 has no cap on the view count. Up to 64 views one block holds
+    the Gram matrix; beyond, one block a view computes the metrics (64 and 65 straddle the
+    switch; 300 views span two 256-view chunks of the similarity sum). The choice and the
+    outputs must match the oracle's."""
+    path, w = da3_weights[1.0]
+    images = synth.procedural_images(views, 28, 42, seed=12)
+    report("da3.refview.many", views=views)
+    out, _ = _run(ctx, path, "f32", images, specs.REF_SADDLE)
+    ref, _ = _oracle(w, images, specs.REF_SADDLE)
+    report("da3.refview.many.choice", got=out["reference_view"], want=ref["reference_view"])
+    assert ref["reference_view"] not in (0, views // 2)  # a choice the fixed strategies would not make
+    _check_fp32(out, ref)
+
+
 def test_da3_two_views_keep_first(ctx, da3_weights):
     path, w = da3_weights[1.0]
     images = synth.procedural_images(2, 42, 42, seed=10)
