@@ -1520,9 +1520,246 @@ static bool launch_f32_auto(const Exec& ex, const GemmArgs& a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// 3x3 stride-1 convolutions with Cin and Cout in {32, 64}, 16-bit types: the DPT heads of the
+// small models (the fusion units, output and ray convolutions of DA3-Small, up to full image
+// resolution). On the per-tap tiles these read every input pixel nine times through the load
+// path for only 32-64 output channels. Here a persistent block keeps the whole filter
+// [Cout][9 Cin] in LDS and walks output tiles of 8 rows x 32 columns of one view: each tile's
+// input halo (10 x 34 pixels, zeros outside the view) streams into one of NBUF LDS buffers
+// ahead of its use, and the nine taps take their A fragments from the halo at shifted pixels.
+// Eight compute waves, one tile row each, Cout / 32 accumulators of 32 pixels x 32 channels,
+// and a ninth wave that only issues the direct-to-LDS loads (filter, halos) and waits for them,
+// so that the compute waves never wait on the memory counter: their epilogue loads and stores
+// stay in flight across tiles. Two block barriers a tile: A (the tile's halo is resident) and C
+// (every compute wave is past its reads of it). The loader issues tile it + NBUF - 1's halo
+// after barrier A of tile it, into the buffer that tile it - 1 left (its epilogue slabs, staged
+// in its own halo buffer, were done before barrier A).
+// LDS: filter rows of 9 Cin elements padded to an odd number of 16-byte chunks, so that the 16
+// rows of a fragment-read phase land on 16 distinct 4-bank groups; halo pixel q keeps chunk c in
+// slot c ^ ((q >> SHP) & (CPP - 1)), so that 16 consecutive pixels do.
+template <typename T, int CIN, int COUT, bool RELU>
+__global__ void __launch_bounds__(576, 1) conv3x3_halo_kernel(const GemmArgs p, int tiles_x, int tiles_y) {
+  constexpr int TH = 8, TW = 32, HC = TW + 2, HR = TH + 2;
+  constexpr int CPP = CIN * 2 / 16;  // 16-byte chunks a pixel: 8 or 4
+  constexpr int SHP = CPP == 8 ? 1 : 2;
+  constexpr int HCH = HR * HC * CPP;  // chunks of a halo
+  constexpr int NDMA = (HCH + 63) / 64;  // DMA instructions a halo, 1 KiB each
+  constexpr int HBUF = NDMA * 1024;
+  constexpr int WCH = 9 * CIN * 2 / 16, WCHP = WCH | 1;  // chunks of a filter row, and its LDS stride
+  constexpr int WLD = WCHP * 16;
+  constexpr int WDMA = (COUT * WCHP + 63) / 64;
+  constexpr int HALO0 = WDMA * 1024;
+  constexpr int NBUF = CIN == 64 ? 2 : 3;
+  constexpr int SLD = slab_ld(1);
+  constexpr int STG = 8 * 32 * SLD * 4;  // the eight compute waves' epilogue slabs
+  constexpr bool STG_IN_HALO = HBUF >= STG;
+  constexpr int LDS = HALO0 + NBUF * HBUF + (STG_IN_HALO ? 0 : STG);
+  static_assert(LDS <= 160 * 1024, "LDS");
+  static_assert(NDMA <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[LDS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int per_view = tiles_x * tiles_y, tiles = p.V * per_view;
+  const int G = gridDim.x, t0 = blockIdx.x;
+  if (t0 >= tiles) return;  // the launcher sizes the grid to at most the tile count
+  const int ntile = (tiles - t0 + G - 1) / G;  // this block's tiles: t0, t0 + G, ...
+
+  const int32x4_t ra = make_rsrc(p.A, uint32_t(long(p.V) * p.Hi * p.Wi * CIN * 2));
+  // Halo of the block's tile it: its origin (view v, input pixel (y0, x0)) and LDS buffer.
+  auto tile_origin = [&](int it, int& y0, int& x0, int& ob) {
+    const int u = t0 + it * G;
+    const int v = u / per_view, r = u - v * per_view, ty = r / tiles_x, tx = r - ty * tiles_x;
+    y0 = ty * TH - 1;
+    x0 = tx * TW - 1;
+    ob = ((v * p.Hi + y0) * p.Wi + x0) * (CIN * 2);  // byte offset of the origin (negative at a border)
+  };
+  // DMA instruction ins of a halo: lane chunk q = 64 ins + lane, halo pixel px = q / CPP at
+  // (hr, hc), its slot q % CPP holding chunk slot ^ ((px >> SHP) & (CPP - 1)) of the pixel
+  auto halo_lane = [&](int ins, int& hr, int& hc, int& rel) {
+    const int q = ins * 64 + lane, px = q / CPP, sl = q - px * CPP;
+    hr = q < HCH ? px / HC : HR;  // HR: a chunk past the halo, read as zeros
+    hc = px - (px / HC) * HC;
+    rel = ((px / HC) * p.Wi + hc) * (CIN * 2) + (sl ^ ((px >> SHP) & (CPP - 1))) * 16;
+  };
+  {
+    // prologue, every wave: its share of the filter (LDS chunk q = row n, chunk c; the padding
+    // chunk reads as zeros) and of tile 0's halo
+    const int32x4_t rw = make_rsrc(p.W, uint32_t(long(p.N) * p.ldw * 2));
+    for (int ins = wave; ins < WDMA; ins += 9) {
+      const int q = ins * 64 + lane, n = q / WCHP, c = q - n * WCHP;
+      const uint32_t off = (n < COUT && c < WCH) ? uint32_t(long(n) * p.ldw * 2 + c * 16) : OOB;
+      load_to_lds(rw, off, 0u, lds_addr(smem) + ins * 1024);
+    }
+    int y0, x0, ob;
+    tile_origin(0, y0, x0, ob);
+    for (int ins = wave; ins < NDMA; ins += 9) {
+      int hr, hc, rel;
+      halo_lane(ins, hr, hc, rel);
+      const bool ok = hr < HR && unsigned(y0 + hr) < unsigned(p.Hi) && unsigned(x0 + hc) < unsigned(p.Wi);
+      load_to_lds(ra, ok ? uint32_t(ob + rel) : OOB, 0u, lds_addr(smem + HALO0) + ins * 1024);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();  // the filter and tile 0's halo are resident
+  }
+
+  if (wave == 8) {
+    // loader wave: each DMA lane's halo pixel and relative offset, once
+    int lhr[NDMA], lhc[NDMA], lrel[NDMA];
+#pragma unroll
+    for (int ins = 0; ins < NDMA; ++ins) halo_lane(ins, lhr[ins], lhc[ins], lrel[ins]);
+    auto issue_halo = [&](int it) {
+      int y0, x0, ob;
+      tile_origin(it, y0, x0, ob);
+      const uint32_t base = lds_addr(smem + HALO0 + (it % NBUF) * HBUF);
+      if (y0 >= 0 && y0 + HR <= p.Hi && x0 >= 0 && x0 + HC <= p.Wi) {  // interior tile: every pixel inside
+#pragma unroll
+        for (int ins = 0; ins < NDMA; ++ins)
+          load_to_lds(ra, lhr[ins] < HR ? uint32_t(ob + lrel[ins]) : OOB, 0u, base + ins * 1024);
+      } else {
+#pragma unroll
+        for (int ins = 0; ins < NDMA; ++ins) {
+          const bool ok = lhr[ins] < HR && unsigned(y0 + lhr[ins]) < unsigned(p.Hi) &&
+                          unsigned(x0 + lhc[ins]) < unsigned(p.Wi);
+          load_to_lds(ra, ok ? uint32_t(ob + lrel[ins]) : OOB, 0u, base + ins * 1024);
+        }
+      }
+    };
+    for (int it = 1; it < NBUF - 1 && it < ntile; ++it) issue_halo(it);
+    for (int it = 0; it < ntile; ++it) {
+      // tile it's halo has landed once only the halos issued after it may be in flight (tile 0's
+      // landed in the prologue)
+      const int later = min(ntile - 1 - it, NBUF - 2);
+      if (later >= 1) wait_vmcnt<NDMA>();
+      else wait_vmcnt<0>();
+      __syncthreads();  // A
+      if (it + NBUF - 1 < ntile) issue_halo(it + NBUF - 1);
+      __syncthreads();  // C
+    }
+    return;
+  }
+
+  // compute waves
+  const int g = lane >> 5, l32 = lane & 31;
+  // per-lane bias: channels j * 32 + (lane & 3) * 8 + 0..7
+  float bs[COUT / 32][8];
+#pragma unroll
+  for (int j = 0; j < COUT / 32; ++j) {
+    const int n = j * 32 + (lane & 3) * 8;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) bs[j][k] = p.bias ? p.bias[n + k] : 0.f;
+  }
+  const bool rf = p.res_f32 != 0, rf2 = p.res2_f32 != 0;
+  for (int it = 0; it < ntile; ++it) {
+    const int t = t0 + it * G;
+    const int cur = it % NBUF;
+    __syncthreads();  // A: this tile's halo is resident
+    f32x16 acc[COUT / 32];
+#pragma unroll
+    for (int j = 0; j < COUT / 32; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+    const char* hb = smem + HALO0 + cur * HBUF;
+    // k-step s = (tap, 16-channel group kk); its fragments are read two steps ahead into one of
+    // three register slots, so that the LDS latency hides behind two steps of MFMAs
+    constexpr int KK = CIN / 16, NSTEP = 9 * KK, NJ = COUT / 32, PF = 2;
+    uint4 fa[PF + 1], fb[PF + 1][NJ];
+    auto read_step = [&](int st, int slot) {
+      const int tap = st / KK, kk = st - tap * KK;
+      const int px = (wave + tap / 3) * HC + l32 + tap % 3;  // halo pixel of this lane's A row
+      const int c = 2 * kk + g;
+      fa[slot] = *reinterpret_cast<const uint4*>(hb + (px * CPP + (c ^ ((px >> SHP) & (CPP - 1)))) * 16);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        fb[slot][j] = *reinterpret_cast<const uint4*>(smem + (j * 32 + l32) * WLD + (tap * (CIN / 8) + c) * 16);
+    };
+#pragma unroll
+    for (int st = 0; st < PF; ++st) read_step(st, st);
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + PF < NSTEP) {
+        read_step(st + PF, (st + PF) % (PF + 1));
+        __builtin_amdgcn_sched_group_barrier(0x100, 1 + NJ, 0);  // the reads first
+      }
+      uint4 a = fa[st % (PF + 1)];
+      if constexpr (RELU) a = Mfma<T>::relu(a);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) Mfma<T>::mma(acc[j], a, fb[st % (PF + 1)][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // C: every compute wave is past its reads of this halo
+    float* slab = reinterpret_cast<float*>(smem + HALO0 + (STG_IN_HALO ? cur * HBUF : NBUF * HBUF)) + wave * 32 * SLD;
+    const int v = t / per_view, r = t - v * per_view, ty = r / tiles_x, tx = r - ty * tiles_x;
+    const int oy = ty * TH + wave;
+    // the epilogue of GemmArgs (epi8's order; no LayerScale on this path): bias, act, table,
+    // residuals, act_post
+#pragma unroll
+    for (int j = 0; j < COUT / 32; ++j) {
+      // accumulator layout: lane l, register r -> pixel 8 (r / 4) + 4 (l / 32) + r % 4, channel l % 32
+#pragma unroll
+      for (int r2 = 0; r2 < 16; ++r2) slab[(8 * (r2 >> 2) + 4 * g + (r2 & 3)) * SLD + l32] = acc[j][r2];
+      slab_done();
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int pix = (lane + 64 * h) >> 2, n = j * 32 + (lane & 3) * 8;
+        const int ox = tx * TW + pix;
+        if (oy < p.Ho && ox < p.Wo) {
+          const long m = (long(v) * p.Ho + oy) * p.Wo + ox;
+          float x[8], tt[8];
+          read8(slab + pix * SLD + (lane & 3) * 8, x);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) x[k] += bs[j][k];
+          if (p.act == ACT_RELU) for (int k = 0; k < 8; ++k) x[k] = fmaxf(x[k], 0.f);
+          else if (p.act == ACT_GELU) for (int k = 0; k < 8; ++k) x[k] = gelu_erf(x[k]);
+          if (p.addtab) { load8<T>(p.addtab, (m % p.addtab_period) * p.N + n, true, tt); for (int k = 0; k < 8; ++k) x[k] += tt[k]; }
+          if (p.res) { load8<T>(p.res, m * p.ldres + n, rf, tt); for (int k = 0; k < 8; ++k) x[k] += tt[k]; }
+          if (p.res2) { load8<T>(p.res2, m * p.ldres2 + n, rf2, tt); for (int k = 0; k < 8; ++k) x[k] += tt[k]; }
+          if (p.act_post == ACT_GELU) for (int k = 0; k < 8; ++k) x[k] = gelu_erf(x[k]);
+          else if (p.act_post == ACT_RELU) for (int k = 0; k < 8; ++k) x[k] = fmaxf(x[k], 0.f);
+          store8<T>(p, x, m * p.ldc + n);
+        }
+      }
+      slab_done();
+    }
+  }
+}
+
+// Which convolutions take conv3x3_halo_kernel: 3x3, stride 1, padding 1, Cin and Cout 32 or 64,
+// plain row stores without LayerScale, 16-byte aligned epilogue operands, and rows of at least
+// 64 pixels (narrower maps waste most of a 32-column tile).
+static bool conv_halo_ok(const GemmArgs& a) {
+  return a.amode == A_CONV && a.ks == 3 && a.stride == 1 && a.pad == 1 && a.Ho == a.Hi && a.Wo == a.Wi &&
+         (a.Cin == 32 || a.Cin == 64) && (a.N == 32 || a.N == 64) && a.store == STORE_ROWS && !a.rm_P && !a.hw3 &&
+         !a.ln_in && !a.ln_out && !a.qk_dim && !a.glu && !a.q_cols && !a.gamma && a.epi_vec && a.Wo >= 64 &&
+         double(a.V) * a.Hi * a.Wi * a.Cin * 2 < 2147483648.0;
+}
+
+template <typename T, int CIN, int COUT>
+static void launch_conv_halo_c(const Exec& ex, const GemmArgs& a, int tx, int ty, int grid) {
+  if (a.relu_in) hipLaunchKernelGGL((conv3x3_halo_kernel<T, CIN, COUT, true>), dim3(grid), dim3(576), 0, ex.stream, a, tx, ty);
+  else hipLaunchKernelGGL((conv3x3_halo_kernel<T, CIN, COUT, false>), dim3(grid), dim3(576), 0, ex.stream, a, tx, ty);
+}
+
+template <typename T>
+static void launch_conv_halo(const Exec& ex, const GemmArgs& a) {
+  const int tx = cdiv(a.Wo, 32), ty = cdiv(a.Ho, 8);
+  const long tiles = long(a.V) * tx * ty;
+  const int grid = int(std::min<long>(tiles, GEMM_CUS));
+  if (a.Cin == 64 && a.N == 64) launch_conv_halo_c<T, 64, 64>(ex, a, tx, ty, grid);
+  else if (a.Cin == 64) launch_conv_halo_c<T, 64, 32>(ex, a, tx, ty, grid);
+  else if (a.N == 64) launch_conv_halo_c<T, 32, 64>(ex, a, tx, ty, grid);
+  else launch_conv_halo_c<T, 32, 32>(ex, a, tx, ty, grid);
+  SPLAT_HIP(hipGetLastError());
+}
+
 // The 16-bit types (bf16, f16) share the tile configurations.
 template <typename H>
 static bool launch_h16_auto(const Exec& ex, const GemmArgs& a) {
+  if (conv_halo_ok(a)) {
+    launch_conv_halo<H>(ex, a);
+    return false;
+  }
   const BfCfg c = pick_bf16(a);
   int S = split_factor(a, c);
   if (S > 1 && !(ex.ws && ex.ws->ptr && ex.ws->cap >= split_bytes(a, S))) S = 1;

@@ -259,6 +259,16 @@ CONV_CASES = [
     # output channels
     (2, 40, 50, 32, 32, 3, 1, 0, 1, False),
     (3, 64, 80, 32, 24, 3, 1, 0, 0, True),
+    # 3x3 stride 1 with Cin and Cout in {32, 64} and rows of at least 64 pixels (the DA3-Small
+    # heads): the persistent halo kernel (16-bit types), tiles of 8 x 32 pixels with ragged last
+    # rows and columns; ReLU-on-load + ReLU, a residual, every Cin / Cout pair, and 260 tiles
+    # (blocks that take two)
+    (2, 108, 144, 64, 64, 3, 1, 1, 1, False),
+    (2, 108, 144, 64, 64, 3, 1, 0, 0, True),
+    (3, 72, 96, 64, 32, 3, 1, 0, 0, False),
+    (2, 70, 100, 32, 64, 3, 1, 0, 1, False),
+    (1, 126, 168, 32, 32, 3, 1, 1, 1, True),
+    (4, 100, 130, 64, 64, 3, 1, 1, 0, True),
 ]
 H16_ONLY = {(3, 112, 148, 96, 256), (3, 88, 94, 96, 256), (6, 112, 148, 128, 256), (6, 112, 148, 96, 256)}
 
@@ -266,6 +276,8 @@ H16_ONLY = {(3, 112, 148, 96, 256), (3, 88, 94, 96, 256), (6, 112, 148, 128, 256
 def bf16_tile(M, N, conv):
     """The 16-bit tile the library's picker (gemm.hip pick_bf16) chooses for an M x N launch:
     the fewest rounds of 256 CUs weighted by each tile's relative per-flop cost."""
+    if conv == "halo":
+        return "halo 8x32"
     if N <= 32:
         return "128x32"
     if N <= 64:
@@ -282,6 +294,13 @@ def bf16_tile(M, N, conv):
     return pick
 
 
+def _conv_kind(ks, stride, Cin, Cout, Wo):
+    """gemm.hip conv_halo_ok: which 16-bit convolutions take the halo kernel."""
+    if ks == 3 and stride == 1 and Cin in (32, 64) and Cout in (32, 64) and Wo >= 64:
+        return "halo"
+    return ks > 1
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("V,H,W,Cin,Cout,ks,stride,relu_in,act,residual", CONV_CASES)
 def test_conv2d_matches_torch(ctx, dtype, V, H, W, Cin, Cout, ks, stride, relu_in, act, residual):
@@ -290,7 +309,7 @@ def test_conv2d_matches_torch(ctx, dtype, V, H, W, Cin, Cout, ks, stride, relu_i
     pad = ks // 2
     Ho, Wo = (H + 2 * pad - ks) // stride + 1, (W + 2 * pad - ks) // stride + 1
     report("conv2d", dtype=dtype, V=V, H=H, W=W, Cin=Cin, Cout=Cout, ks=ks, stride=stride,
-           tile=bf16_tile(V * Ho * Wo, Cout, ks > 1) if dtype != "f32" else "fp32")
+           tile=bf16_tile(V * Ho * Wo, Cout, _conv_kind(ks, stride, Cin, Cout, Wo)) if dtype != "f32" else "fp32")
     code, tdt = _dt(dtype)
     F = torch.nn.functional
     g = torch.Generator().manual_seed(V * 31 + H * 7 + Cin + Cout)
