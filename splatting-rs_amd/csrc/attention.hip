@@ -407,8 +407,32 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   // run on one XCD
   const int nq = (L + WAVES * QT * 32 - 1) / (WAVES * QT * 32);
   const int ns = SPLIT ? p.nsplit : 1;
-  const int id = xcd_contiguous(blockIdx.x, nq * ns * p.heads * p.seqs);
-  const int qb = id % nq, split = (id / nq) % ns, h = (id / (nq * ns)) % p.heads, sq = id / (nq * ns * p.heads);
+  int qb, split, h, sq;
+  bool whole = !SPLIT;  // the block covers every key tile and writes the output itself
+  if (SPLIT && p.whole > 0) {
+    // Tail split: (query block, head, sequence) units t < p.whole run whole, the rest in ns key
+    // slices; each group is dealt to the XCDs on its own (p.whole is a multiple of 8)
+    const int b = blockIdx.x;
+    int t;
+    if (b < p.whole) {
+      t = xcd_contiguous(b, p.whole);
+      split = 0;
+      whole = true;
+    } else {
+      const int r = xcd_contiguous(b - p.whole, (nq * p.heads * p.seqs - p.whole) * ns);
+      t = p.whole + r / ns;
+      split = r % ns;
+    }
+    qb = t % nq;
+    h = (t / nq) % p.heads;
+    sq = t / (nq * p.heads);
+  } else {
+    const int id = xcd_contiguous(blockIdx.x, nq * ns * p.heads * p.seqs);
+    qb = id % nq;
+    split = (id / nq) % ns;
+    h = (id / (nq * ns)) % p.heads;
+    sq = id / (nq * ns * p.heads);
+  }
   const long base = long(sq) * p.seq_stride;
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + h * 64;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + h * 64;
@@ -626,7 +650,7 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
   };
 
   const int ntiles = (L + 63) / 64;
-  const int t0 = SPLIT ? split * p.tps : 0, t1 = SPLIT ? min(ntiles, t0 + p.tps) : ntiles;
+  const int t0 = whole ? 0 : split * p.tps, t1 = whole ? ntiles : min(ntiles, t0 + p.tps);
   const std::integral_constant<int, 0> R0;
   const std::integral_constant<int, 1> R1;
   // One pass over the slice's key tiles. Every tile but the last runs without the key mask (a
@@ -689,7 +713,7 @@ __global__ void __launch_bounds__(WAVES * 64, QT == 1 ? 4 : 2) attn_bf16_kernel(
     const auto l2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum[qt]), __float_as_uint(lsum[qt]), false, false);
     const float tot = __uint_as_float(l2[0]) + __uint_as_float(l2[1]);
     const int qrow = q0 + qt * 32 + l32;
-    if constexpr (SPLIT) {
+    if (SPLIT && !whole) {
       if (qrow < L) {
         const long row = long(sq) * L + qrow, rows = long(p.seqs) * L;  // dense slice rows
         float* O = p.part + (long(split) * rows + row) * (long(p.heads) * 64) + h * 64;
@@ -925,6 +949,11 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnArgs p) {
   if (id >= rows * p.heads * 8) return;
   const long row = id / (p.heads * 8);
   const int rem = int(id - row * p.heads * 8), h = rem >> 3, c8 = (rem & 7) * 8;
+  if (p.whole > 0) {  // tail split: the whole units wrote their output themselves
+    const long sq = row / p.L;
+    const int nq = (p.L + p.qrows - 1) / p.qrows;
+    if ((sq * p.heads + h) * nq + int(row - sq * p.L) / p.qrows < p.whole) return;
+  }
   const long so = rows * p.heads * 64;
   const float* ml = p.part + long(p.nsplit) * so;
   // every slice's loads go out before any is used (one memory latency, not nsplit of them);
@@ -1001,7 +1030,7 @@ static void launch16(const Exec& ex, const AttnArgs& b, float c, bool fast, bool
     }
     return;
   }
-  const dim3 grid(unsigned(blocks * b.nsplit));
+  const dim3 grid(unsigned(b.whole > 0 ? b.whole + (blocks - b.whole) * b.nsplit : blocks * b.nsplit));
   if (b.nsplit > 1) {
     if (qt2) hipLaunchKernelGGL((attn_bf16_kernel<4, 2, true, H>), grid, dim3(256), 0, ex.stream, b, c);
     else hipLaunchKernelGGL((attn_bf16_kernel<4, 1, true, H>), grid, dim3(256), 0, ex.stream, b, c);
@@ -1048,9 +1077,27 @@ void attention(const Exec& ex, const AttnArgs& a) {
   const long blocks = qt2 ? blocks2 : blocks1;
   // the fp32 kernel's 32-key tiles: slices of at least 4 tiles, about two blocks per CU
   const int ntiles = f32_fast ? cdiv(a.L, 32) : cdiv(a.L, 64);
-  const int S = bf_fast    ? (a.L >= 4096 ? attn_splits(blocks, ntiles, qt2) : 1)
+  int S = bf_fast    ? (a.L >= 4096 ? attn_splits(blocks, ntiles, qt2) : 1)
                 : f32_fast ? int(std::min<long>(std::min<long>(8, std::max(1, ntiles / 4)), std::max<long>(1, cdiv(512, gblocks))))
                            : int(std::min<long>(std::min<long>(8, ntiles / 2), std::max<long>(1, cdiv(512, gblocks))));
+  // Tail split: a QT=1 grid just past whole rounds of 256 blocks (all resident, at most four a
+  // CU) runs those rounds whole and only the tail in key slices, so that each CU gets about the
+  // same work (C4 global, 588 blocks: 512 whole, 76 in 3 slices, instead of 76 CUs with a third
+  // whole block). Modelled like attn_splits, with 5% margin for the partials of the tail.
+  int whole = 0;
+  if (bf_fast && a.L >= 4096 && !qt2 && S == 1 && blocks > 512 && blocks <= 4 * 256) {
+    const long full = blocks / 256 * 256, tail = blocks - full;
+    double best = 1e30;
+    int bs = 1;
+    for (int s2 = 2; s2 <= 4 && ntiles / s2 >= 8; ++s2) {
+      const double cost = std::ceil(double(tail) * s2 / 256.0) / s2 * (1.0 + 0.02 * s2);
+      if (cost < best * 0.999) { best = cost; bs = s2; }
+    }
+    if (tail > 0 && bs > 1 && double(full / 256) + best < 0.95 * double((blocks + 255) / 256)) {
+      S = bs;
+      whole = int(full);
+    }
+  }
   AttnArgs b = a;
   if (S > 1) {
     b.tps = cdiv(ntiles, S);
@@ -1060,6 +1107,10 @@ void attention(const Exec& ex, const AttnArgs& a) {
     if (ex.dry && ex.ws) ex.ws->need = std::max(ex.ws->need, need);
     if (!ex.dry && !(ex.ws && ex.ws->ptr && ex.ws->cap >= need)) b.nsplit = 1;  // not sized: one slice
     b.part = b.nsplit > 1 ? static_cast<float*>(ex.ws->ptr) : nullptr;
+    if (b.nsplit > 1 && whole > 0) {
+      b.whole = whole;
+      b.qrows = 128;  // QT = 1: 4 waves x 32 queries
+    }
   }
   if (ex.dry) return;
   const double rows = double(a.seqs) * a.L * a.heads;

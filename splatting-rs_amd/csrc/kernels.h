@@ -113,6 +113,10 @@ struct AttnArgs {
   // holds the unnormalised fp32 O of every slice, [nsplit][seqs*L][heads*64], then each
   // slice's (exponent reference, sum) per query and head, [nsplit][seqs*L][heads][2].
   int nsplit = 1, tps = 0; float* part = nullptr;
+  // Tail split (a bf16/f16 launch with nsplit > 1): the first `whole` (query block, head,
+  // sequence) units, query blocks of qrows queries fastest, run over every key tile and write O
+  // themselves; only the remaining units run in slices (and go through part).
+  int whole = 0, qrows = 0;
   // Q already multiplied by log2(e)/8 (ATTN_Q_SCALE) and rounded once; otherwise the bf16
   // kernel multiplies each Q element by it and rounds it to bf16 again (a second rounding).
   int q_scaled = 0;
