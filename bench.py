@@ -217,6 +217,80 @@ def time_host_io(ctx, cfg, seed, reps):
     return 1e3 * (time.perf_counter() - t) / reps
 
 
+# (M, N, K, epilogue): the transformer layers' GEMMs of the benchmark configurations. "ln": a
+# folded-LayerNorm consumer (qkv, or fc1 with GELU), "res": a residual producer with row
+# statistics and a bf16 copy (proj, fc2). M = 6222 (C4: 6 views of 1037 encoder tokens), 6223 (C4
+# info-sharing, 6 x 1037 + 1), 5838 (C2: 6 x 973).
+GEMM_SHAPES = [(6222, 3072, 1024, "ln"), (6222, 1024, 1024, "res"), (6222, 4096, 1024, "ln-gelu"),
+               (6222, 1024, 4096, "res"), (6223, 2304, 768, "ln"), (6223, 768, 768, "res"),
+               (6223, 3072, 768, "ln-gelu"), (6223, 768, 3072, "res"), (5838, 1152, 384, "ln"),
+               (5838, 384, 384, "res"), (5838, 1536, 384, "ln-gelu"), (5838, 384, 1536, "res"),
+               (8192, 8192, 8192, "plain")]
+
+
+def gemm_vs_hipblaslt(torch, splathip):
+    """The library's bf16 GEMM (splat_kernel_gemm, bias epilogue; splat_kernel_gemm_ln, the fused
+    epilogue the forward uses) against torch.addmm on the same operands (rocBLAS/hipBLASLt), each
+    timed with events around 50 back-to-back launches (10 for 8192^3) after 5 warm-up ones."""
+    ctx = splathip.Context(0)
+    ours = torch.cuda.ExternalStream(ctx.stream)
+    dt, tdt = splathip.BF16, torch.bfloat16
+
+    def timed(fn, stream, reps):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        ctx.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ctx.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for (M, N, K, epi) in GEMM_SHAPES:
+        reps = 10 if M == 8192 else 50
+        A = torch.randn(M, K, device="cuda", generator=g).to(tdt)
+        W = (torch.randn(N, K, device="cuda", generator=g) * 0.05).to(tdt)
+        b = torch.randn(N, device="cuda", generator=g)
+        out = torch.empty(M, N, device="cuda", dtype=tdt)
+        bt = b.to(tdt)
+        torch.cuda.synchronize()
+        t_plain = timed(lambda: ctx.kernel_gemm(dt, A.data_ptr(), M, K, W.data_ptr(), N, K, b.data_ptr(), 0,
+                                                out.data_ptr(), False), ours, reps)
+        t_lib = timed(lambda: torch.addmm(bt, A, W.t(), out=out), torch.cuda.current_stream(), reps)
+        t_fused = None
+        if epi.startswith("ln"):
+            c1 = torch.randn(N, device="cuda", generator=g)
+            st = torch.rand(M, K // 64, 2, device="cuda", generator=g) + 1
+            act = 2 if epi == "ln-gelu" else 0
+            torch.cuda.synchronize()
+            t_fused = timed(lambda: ctx.kernel_gemm_ln(dt, A.data_ptr(), M, K, W.data_ptr(), N, K, b.data_ptr(), act,
+                                                       out.data_ptr(), False, ln_in=st.data_ptr(), c1=c1.data_ptr(),
+                                                       eps=1e-6, group=64), ours, reps)
+        elif epi == "res":
+            gm = torch.rand(N, device="cuda", generator=g)
+            r = torch.randn(M, N, device="cuda", generator=g)
+            o32 = torch.empty(M, N, device="cuda")
+            stats = torch.empty(M, N // 64, 2, device="cuda")
+            cp = torch.empty(M, N, device="cuda", dtype=tdt)
+            torch.cuda.synchronize()
+            t_fused = timed(lambda: ctx.kernel_gemm_ln(dt, A.data_ptr(), M, K, W.data_ptr(), N, K, b.data_ptr(), 0,
+                                                       o32.data_ptr(), True, gamma=gm.data_ptr(), res=r.data_ptr(),
+                                                       ln_out=stats.data_ptr(), copy=cp.data_ptr(), group=64),
+                            ours, reps)
+        fl = 2.0 * M * N * K
+        line = {"shape": [M, N, K], "epilogue": epi, "ours_plain_us": round(t_plain, 2),
+                "hipblaslt_us": round(t_lib, 2), "ours_plain_tflops": round(fl / t_plain / 1e6, 1),
+                "hipblaslt_tflops": round(fl / t_lib / 1e6, 1)}
+        if t_fused is not None:
+            line["ours_fused_us"] = round(t_fused, 2)
+        print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -234,6 +308,10 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB -> 256 MiB streaming kernel (torch.neg on fp32), the "
                          "reference that scales FETCH_SIZE / WRITE_SIZE counter runs to bytes")
+    ap.add_argument("--gemm-vs-hipblaslt", action="store_true",
+                    help="instead of the forward: time the library's GEMM on the network's layer shapes (plain "
+                         "bias epilogue, then the forward's fused epilogue) next to torch.matmul on the same "
+                         "shapes (hipBLASLt), one JSON line per shape")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the network would "
@@ -247,6 +325,9 @@ def main():
     from splathip import specs, synth
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.gemm_vs_hipblaslt:
+        gemm_vs_hipblaslt(torch, splathip)
+        return
     if args.copy_calibration:
         src = torch.ones(COPY_CAL_BYTES // 4, device="cuda")
         dst = torch.empty_like(src)
