@@ -1049,21 +1049,23 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
   constexpr bool SPREAD = STAGES >= 3;
   constexpr int AHEAD = SPREAD ? STAGES - 1 : STAGES;  // tile kt loads tile kt + AHEAD
   // Folded LayerNorm: thread r < BM loads the partial statistics of tile row r ahead of the
-  // operand tiles (up to 16 pairs) and reduces them once those tiles are resident.
+  // operand tiles (up to 16 pairs) and reduces them once the first stage is resident.
+  // The loads are unconditional (a clamped row and partial; the zeros are applied afterwards) so
+  // that the compiler issues all of them back to back, not each behind its own wait.
   float2 lnv[EPI == EPI_LN ? 16 : 1];
   const long lnm = m0 + tid;
   if constexpr (EPI == EPI_LN) {
+    const float* lrow = p.ln_in + (tid < BM && lnm < p.M ? lnm : 0) * p.ln_parts * 2;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) lnv[j] = *reinterpret_cast<const float2*>(lrow + min(j, p.ln_parts - 1) * 2);
 #pragma unroll
     for (int j = 0; j < 16; ++j)
-      lnv[j] = (tid < BM && lnm < p.M && j < p.ln_parts)
-                   ? *reinterpret_cast<const float2*>(p.ln_in + (lnm * p.ln_parts + j) * 2)
-                   : make_float2(0.f, 0.f);
+      if (j >= p.ln_parts) lnv[j] = make_float2(0.f, 0.f);
   }
+  // Stage 0, then the row statistics (the compiler's wait for their loads also covers the DMA
+  // loads issued before it, which tile 0 needs anyway), then the later stages.
 #pragma unroll
-  for (int s = 0; s < AHEAD; ++s)
-#pragma unroll
-    for (int l = 0; l < LPT; ++l) issue_one(s, s, l, std::false_type{});
-  wait_vmcnt<(AHEAD - 1) * LPT>();
+  for (int l = 0; l < LPT; ++l) issue_one(0, 0, l, std::false_type{});
   float ln_rstd = 0.f, ln_shift = 0.f;
   if constexpr (EPI == EPI_LN) {
     if (tid < BM) {
@@ -1082,6 +1084,11 @@ __global__ void __launch_bounds__(WM * WN * 64, MINB) gemm_mfma_kernel(const Gem
       }
     }
   }
+#pragma unroll
+  for (int s = 1; s < AHEAD; ++s)
+#pragma unroll
+    for (int l = 0; l < LPT; ++l) issue_one(s, s, l, std::false_type{});
+  wait_vmcnt<(AHEAD - 1) * LPT>();
   __syncthreads();
   // fp32 tiles share a CU two or four at a time: a block in its main loop issues ahead of a
   // block in its prologue or epilogue (C1 -0.3%; for the 16-bit tiles, mostly one a CU, the same
