@@ -1080,20 +1080,22 @@ void attention(const Exec& ex, const AttnArgs& a) {
   int S = bf_fast    ? (a.L >= 4096 ? attn_splits(blocks, ntiles, qt2) : 1)
                 : f32_fast ? int(std::min<long>(std::min<long>(8, std::max(1, ntiles / 4)), std::max<long>(1, cdiv(512, gblocks))))
                            : int(std::min<long>(std::min<long>(8, ntiles / 2), std::max<long>(1, cdiv(512, gblocks))));
-  // Tail split: a QT=1 grid just past whole rounds of 256 blocks (all resident, at most four a
-  // CU) runs those rounds whole and only the tail in key slices, so that each CU gets about the
-  // same work (C4 global, 588 blocks: 512 whole, 76 in 3 slices, instead of 76 CUs with a third
-  // whole block). Modelled like attn_splits, with 5% margin for the partials of the tail.
+  // Tail split: a grid past whole rounds of 256 blocks runs those rounds whole and only the tail
+  // in key slices, so that each CU gets about the same work without every block paying for
+  // partials and the merge (C4 global, 588 QT=1 blocks: 512 whole, 76 in 3 slices, instead of 76
+  // CUs with a third whole block). Modelled like attn_splits and taken when it beats the plan
+  // above (unsplit, or every block in S slices) by 3%.
   int whole = 0;
-  if (bf_fast && a.L >= 4096 && !qt2 && S == 1 && blocks > 512 && blocks <= 4 * 256) {
+  if (bf_fast && a.L >= 4096 && blocks > 256 && blocks % 256 != 0) {
     const long full = blocks / 256 * 256, tail = blocks - full;
+    const double cur = std::ceil(double(blocks) * S / 256.0) / S * (S > 1 ? 1.0 + 0.02 * S : 1.0);
     double best = 1e30;
     int bs = 1;
     for (int s2 = 2; s2 <= 4 && ntiles / s2 >= 8; ++s2) {
       const double cost = std::ceil(double(tail) * s2 / 256.0) / s2 * (1.0 + 0.02 * s2);
       if (cost < best * 0.999) { best = cost; bs = s2; }
     }
-    if (tail > 0 && bs > 1 && double(full / 256) + best < 0.95 * double((blocks + 255) / 256)) {
+    if (bs > 1 && double(full / 256) + best < 0.97 * cur) {
       S = bs;
       whole = int(full);
     }
@@ -1109,7 +1111,7 @@ void attention(const Exec& ex, const AttnArgs& a) {
     b.part = b.nsplit > 1 ? static_cast<float*>(ex.ws->ptr) : nullptr;
     if (b.nsplit > 1 && whole > 0) {
       b.whole = whole;
-      b.qrows = 128;  // QT = 1: 4 waves x 32 queries
+      b.qrows = qt2 ? 256 : 128;  // 4 waves x QT x 32 queries
     }
   }
   if (ex.dry) return;

@@ -130,10 +130,12 @@ ATTN_CASES = [
     (9, 1100, 12),   # 972 blocks: the same with another ragged end
     # long sequences: key slices merged by a second kernel where the grid leaves block slots idle
     (1, 6223, 12),   # the MapAnything C4 global block (588 blocks: 512 whole, the 76 left in 3 key slices)
-    (1, 4096, 33),   # two query sub-tiles per wave with slices, no ragged tile
+    (1, 4096, 33),   # two query sub-tiles per wave, 528 blocks: 512 whole, 16 in 4 slices, no ragged tile
     # tail splits: two sequences (576 blocks: 512 whole, 64 in 4 slices), and 561 blocks
     (2, 4500, 8),
     (1, 4100, 17),
+    # two query sub-tiles per wave: 544 blocks, 512 whole and 32 in 4 slices, ragged last key tile
+    (2, 4100, 16),
 ]
 
 
@@ -187,7 +189,7 @@ EXTREME_CASES = ["high", "low", "late_peak", "mixed"]
 
 
 @pytest.mark.parametrize("dtype,S,L,heads", [("bf16", 2, 1037, 3), ("bf16", 7, 1037, 16), ("bf16", 1, 6223, 2),
-                                             ("bf16", 2, 4500, 8),
+                                             ("bf16", 2, 4500, 8), ("bf16", 2, 4100, 16),
                                              ("f16", 2, 1037, 3), ("f16", 7, 1037, 16), ("f16", 1, 6223, 2),
                                              ("f32", 1, 1297, 6), ("f32", 3, 130, 2)])
 @pytest.mark.parametrize("kind", EXTREME_CASES)
