@@ -1463,7 +1463,10 @@ static BfCfg pick_bf16(const GemmArgs& a) {
   if (a.amode == A_CONV && a.N == 128 && cdiv(a.M, 192) >= 3 * GEMM_CUS) return CFG_192x128D;
   const BfCfg cands[] = {CFG_256x256, CFG_256x128, CFG_320x256, CFG_320x128, CFG_192x128, CFG_128x128};
   const double eff[] = {1.0, 0.80, 1.0, 0.80, 0.75, 0.65};
+  // On equal cost the fewer, larger rounds win (MapAnything C5's 24888x3072x1024 qkv: five
+  // rounds of 256x256 or four of 320x256, 191 -> 172 us).
   double best = 1e30;
+  long best_rounds = 0;
   BfCfg pick = a.hw3 ? CFG_320x128 : CFG_256x256;
   for (int i = 0; i < 6; ++i) {
     const BfShape sh = bf_shape(cands[i]);
@@ -1471,7 +1474,11 @@ static BfCfg pick_bf16(const GemmArgs& a) {
     const long tiles = long(cdiv(a.M, sh.bm)) * cdiv(a.N, sh.bn);
     const long rounds = (tiles + GEMM_CUS - 1) / GEMM_CUS;
     const double cost = double(rounds) * sh.bm * sh.bn / eff[i];
-    if (cost < best * 0.999) { best = cost; pick = cands[i]; }
+    if (cost < best * 0.999 || (cost <= best * 1.001 && rounds < best_rounds)) {
+      best = cost;
+      best_rounds = rounds;
+      pick = cands[i];
+    }
   }
   return pick;
 }
